@@ -1,0 +1,429 @@
+// fa_api.cpp -- host side of the C ABI declared in include/fa_mi355x.h:
+// validation, split-KV planning, workspace layout and kernel launches.
+//
+// Mirrors the checks and decisions of the reference host code
+// (csrc/arch22/flash_attn_npu_v2/flash_api.cpp: mha_fwd_kvcache :356-626,
+// mha_fwd :628-826, mha_varlen_fwd :828-1060; csrc/arch22/flash_attn_npu_v3/
+// flash_api.cpp: mha_fwd :60-491) without its host round trips: the plan is a
+// function of host-known shapes only, and the per-sequence split is decided on
+// the device from cache_seqlens.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <mutex>
+#include <string>
+
+#include "../../include/fa_mi355x.h"
+#include "fa_kernel_args.h"
+
+namespace fa {
+int fwd_tile_rows(bool decode);
+int fwd_tile_keys(bool decode);
+hipError_t launch_fwd(const FwdArgs& a, int dtype, int d, bool decode, int grid, hipStream_t stream);
+hipError_t launch_combine(const CombineArgs& c, int dtype, int d, int grid, hipStream_t stream);
+hipError_t launch_combine_flat(const float* po, const float* pl, int S, int64_t R, int Dv, void* out, int64_t ors,
+                               int out_dtype, float* lse, hipStream_t stream);
+hipError_t launch_kv_prep(const KvPrepArgs& a, int dtype, hipStream_t stream);
+}  // namespace fa
+
+namespace {
+
+constexpr int kMaxBatch = 2048;   // per-batch plan lives in LDS
+constexpr int kDecodeRows = 16;   // rows per (b, kv head) that take the decode kernel
+
+thread_local std::string g_err;
+
+fa_status_t fail(fa_status_t st, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return st;
+}
+
+#define FA_CHECK(cond, ...)                              \
+    do {                                                 \
+        if (!(cond)) return fail(FA_EINVAL, __VA_ARGS__); \
+    } while (0)
+
+int cu_count() {
+    static std::mutex mu;
+    static int counts[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    std::lock_guard<std::mutex> lk(mu);
+    if (counts[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        counts[dev] = n;
+    }
+    return counts[dev];
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool strides8(int64_t a, int64_t b, int64_t c) { return (a % 8) == 0 && (b % 8) == 0 && (c % 8) == 0; }
+
+struct Plan {
+    bool decode;
+    int BM, BN;
+    int g;
+    int rows_max;       // packed rows per (b, kv head) bound
+    int mt_max;
+    int kv_capacity;
+    bool allow_split;
+    int target_items;
+    int min_chunk;
+    int64_t items_max;  // bound on work items (partial buffer size)
+    int grid;
+    bool rotary;
+    size_t off_sched, off_plse, off_po, off_qrot, total;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+fa_status_t validate(const fa_fwd_params* p, int kind) {
+    FA_CHECK(p != nullptr, "params must not be null");
+    FA_CHECK(p->abi_version == FA_MI355X_ABI_VERSION, "abi_version %d does not match library ABI %d", p->abi_version,
+             FA_MI355X_ABI_VERSION);
+    FA_CHECK(kind == FA_KIND_KVCACHE || kind == FA_KIND_DENSE || kind == FA_KIND_VARLEN, "unknown kind %d", kind);
+    FA_CHECK(p->dtype == FA_DTYPE_FP16 || p->dtype == FA_DTYPE_BF16,
+             "FlashAttention only support fp16 and bf16 data type");
+    FA_CHECK(p->batch >= 1, "batch size must be positive");
+    FA_CHECK(p->batch <= kMaxBatch, "batch size %d exceeds the supported maximum %d", p->batch, kMaxBatch);
+    FA_CHECK(p->nheads >= 1 && p->nheads_k >= 1, "number of heads must be positive");
+    FA_CHECK(p->nheads % p->nheads_k == 0, "Number of heads in key/value must divide number of heads in query");
+    FA_CHECK(p->headdim >= 1, "head dimension must be positive");
+    if (p->headdim != 128)
+        return fail(FA_EUNSUPPORTED, "headdim %d is not supported by this build (supported: 128)", p->headdim);
+    FA_CHECK(p->headdim_v == p->headdim, "headdim_v (%d) must equal headdim (%d)", p->headdim_v, p->headdim);
+    if (p->dropout_p != 0.f) return fail(FA_EUNSUPPORTED, "dropout is not supported (forward inference only)");
+    FA_CHECK(p->softcap >= 0.f, "softcap must be >= 0");
+    FA_CHECK(p->num_splits >= 0, "num_splits must be >= 0");
+    FA_CHECK(p->seqlen_q >= 0, "seqlen_q must be >= 0");
+    FA_CHECK(p->q && p->k && p->v && p->out && p->softmax_lse, "q, k, v, out and softmax_lse must be given");
+    FA_CHECK(aligned16(p->q) && aligned16(p->k) && aligned16(p->v) && aligned16(p->out),
+             "q, k, v and out must be 16-byte aligned");
+    FA_CHECK(strides8(p->q_batch_stride, p->q_row_stride, p->q_head_stride), "q strides must be multiples of 8 elements");
+    FA_CHECK(strides8(p->k_batch_stride, p->k_row_stride, p->k_head_stride), "k strides must be multiples of 8 elements");
+    FA_CHECK(strides8(p->v_batch_stride, p->v_row_stride, p->v_head_stride), "v strides must be multiples of 8 elements");
+    FA_CHECK(strides8(p->out_batch_stride, p->out_row_stride, p->out_head_stride),
+             "out strides must be multiples of 8 elements");
+    if (p->alibi_slopes)
+        FA_CHECK(p->alibi_batch_stride == 0 || p->alibi_batch_stride == p->nheads,
+                 "alibi_slopes must have shape (nheads) or (batch_size, nheads)");
+    if (kind == FA_KIND_KVCACHE) {
+        const bool paged = p->block_table != nullptr;
+        if (paged) {
+            FA_CHECK(p->page_block_size >= 1, "page_block_size must be positive");
+            FA_CHECK(p->max_blocks_per_seq >= 1, "block_table must have at least one column");
+            FA_CHECK(p->batch_cache >= 1, "paged KV cache must have at least one block");
+            FA_CHECK(p->block_table_rows >= (p->cache_batch_idx ? 1 : p->batch), "block_table must have a row per batch entry");
+        } else {
+            FA_CHECK(p->batch_cache >= 1, "k_cache batch must be positive");
+            FA_CHECK(p->seqlen_k >= 1, "k_cache seqlen must be positive");
+            if (!p->cache_batch_idx)
+                FA_CHECK(p->batch_cache >= p->batch, "k_cache batch (%d) smaller than q batch (%d) without cache_batch_idx",
+                         p->batch_cache, p->batch);
+        }
+        FA_CHECK((p->k_new == nullptr) == (p->v_new == nullptr), "If key is supplied, value must also be passed in");
+        if (p->k_new) {
+            FA_CHECK(p->seqlen_new >= 1, "k/v must have at least one new token");
+            FA_CHECK(p->cache_seqlens != nullptr, "cache_seqlens is required to append k/v");
+            FA_CHECK(aligned16(p->k_new) && aligned16(p->v_new), "k and v must be 16-byte aligned");
+        }
+        if (p->rotary_cos || p->rotary_sin) {
+            FA_CHECK(p->rotary_cos && p->rotary_sin, "rotary_cos and rotary_sin must be given together");
+            FA_CHECK(p->k_new != nullptr, "If rotary cos/sin are provided, new key / value to be appended to KV cache must also be provided");
+            FA_CHECK(p->rotary_dim > 0 && p->rotary_dim % 16 == 0, "rotary_dim must be divisible by 16");
+            FA_CHECK(p->rotary_dim <= p->headdim, "rotary_dim must be <= headdim");
+            FA_CHECK(p->seqlen_ro >= 1, "rotary_cos must have at least one row");
+        }
+    } else {
+        FA_CHECK(p->k_new == nullptr && p->v_new == nullptr, "k_new/v_new are only valid for the kvcache forward");
+        FA_CHECK(p->rotary_cos == nullptr && p->rotary_sin == nullptr, "rotary is only valid for the kvcache forward");
+        FA_CHECK(p->block_table == nullptr || kind == FA_KIND_VARLEN, "block_table is not valid for the dense forward");
+        FA_CHECK(p->seqlen_k >= 0, "seqlen_k must be >= 0");
+        if (kind == FA_KIND_VARLEN) {
+            FA_CHECK(p->cu_seqlens_q != nullptr, "cu_seqlens_q is required");
+            FA_CHECK(p->cu_seqlens_k || (p->block_table && p->cache_seqlens),
+                     "cu_seqlens_k is required (or, with a block_table, seqused_k)");
+            FA_CHECK(p->total_q >= 0, "total_q must be >= 0");
+            if (p->block_table) {
+                FA_CHECK(p->page_block_size >= 1 && p->max_blocks_per_seq >= 1 && p->batch_cache >= 1,
+                         "paged varlen needs page_block_size, block_table columns and num_blocks");
+            }
+        }
+    }
+    return FA_OK;
+}
+
+void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
+    pl.g = p->nheads / p->nheads_k;
+    pl.rows_max = p->seqlen_q * pl.g;
+    pl.decode = pl.rows_max <= kDecodeRows;
+    pl.BM = fa::fwd_tile_rows(pl.decode);
+    pl.BN = fa::fwd_tile_keys(pl.decode);
+    pl.mt_max = (pl.rows_max + pl.BM - 1) / pl.BM;
+    if (pl.mt_max < 1) pl.mt_max = 1;
+    if (kind == FA_KIND_KVCACHE) {
+        pl.kv_capacity = p->block_table ? (int)std::min<int64_t>((int64_t)p->max_blocks_per_seq * p->page_block_size, INT_MAX)
+                                        : p->seqlen_k;
+    } else if (kind == FA_KIND_VARLEN) {
+        pl.kv_capacity = p->block_table ? (int)std::min<int64_t>((int64_t)p->max_blocks_per_seq * p->page_block_size, INT_MAX)
+                                        : INT_MAX;
+    } else {
+        pl.kv_capacity = p->seqlen_k;
+    }
+    const int cus = cu_count();
+    const int occ = 2;  // workgroups per CU for both kernel shapes
+    const int64_t base_bound = (int64_t)p->batch * p->nheads_k * pl.mt_max;
+    pl.target_items = (pl.decode ? 8 : 4) * cus;
+    pl.min_chunk = 2 * pl.BN;
+    if (p->num_splits == 1) {
+        pl.allow_split = false;
+    } else if (p->num_splits > 1) {
+        pl.allow_split = true;
+    } else {
+        pl.allow_split = pl.decode || base_bound < cus;
+    }
+    if (!pl.allow_split) pl.items_max = base_bound;
+    else if (p->num_splits > 1) pl.items_max = base_bound * p->num_splits;
+    else pl.items_max = base_bound + pl.target_items;
+    const int64_t persistent = (int64_t)occ * cus;
+    if (pl.allow_split || pl.decode) pl.grid = (int)std::min<int64_t>(pl.items_max, persistent);
+    else pl.grid = (int)std::min<int64_t>(pl.items_max, INT_MAX);
+    if (pl.grid < 1) pl.grid = 1;
+    pl.rotary = kind == FA_KIND_KVCACHE && p->rotary_cos != nullptr;
+
+    size_t off = 0;
+    pl.off_sched = off;
+    off = align256(off + sizeof(int) * (2 * (size_t)p->batch + 2));
+    pl.off_plse = off;
+    if (pl.allow_split) off = align256(off + sizeof(float) * (size_t)pl.items_max * pl.BM);
+    pl.off_po = off;
+    if (pl.allow_split) off = align256(off + sizeof(float) * (size_t)pl.items_max * pl.BM * p->headdim_v);
+    pl.off_qrot = off;
+    if (pl.rotary) off = align256(off + 2 * (size_t)p->batch * p->seqlen_q * p->nheads * p->headdim);
+    pl.total = off;
+}
+
+fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
+    fa_status_t st = validate(p, kind);
+    if (st != FA_OK) return st;
+    hipStream_t stream = static_cast<hipStream_t>(stream_v);
+    Plan pl;
+    make_plan(p, kind, pl);
+    if (p->seqlen_q == 0 && kind != FA_KIND_VARLEN) return FA_OK;
+    if (pl.total > 0) {
+        if (!p->workspace || p->workspace_bytes < pl.total)
+            return fail(FA_EWORKSPACE, "workspace of %zu bytes required, %zu given", pl.total,
+                        p->workspace ? p->workspace_bytes : (size_t)0);
+        if (reinterpret_cast<uintptr_t>(p->workspace) & 255u)
+            return fail(FA_EWORKSPACE, "workspace must be 256-byte aligned");
+    }
+    char* ws = static_cast<char*>(p->workspace);
+    const bool paged = p->block_table != nullptr;
+
+    const void* q_ptr = p->q;
+    int64_t q_sb = p->q_batch_stride, q_si = p->q_row_stride, q_sh = p->q_head_stride;
+
+    if (kind == FA_KIND_KVCACHE && p->k_new) {
+        fa::KvPrepArgs k{};
+        k.k_new = p->k_new;
+        k.kn_sb = p->knew_batch_stride;
+        k.kn_si = p->knew_row_stride;
+        k.kn_sh = p->knew_head_stride;
+        k.v_new = p->v_new;
+        k.vn_sb = p->vnew_batch_stride;
+        k.vn_si = p->vnew_row_stride;
+        k.vn_sh = p->vnew_head_stride;
+        k.k_cache = p->k;
+        k.k_sb = p->k_batch_stride;
+        k.k_si = p->k_row_stride;
+        k.k_sh = p->k_head_stride;
+        k.v_cache = p->v;
+        k.v_sb = p->v_batch_stride;
+        k.v_si = p->v_row_stride;
+        k.v_sh = p->v_head_stride;
+        k.seqlens = p->cache_seqlens;
+        k.batch_idx = p->cache_batch_idx;
+        k.block_table = p->block_table;
+        k.bt_stride = p->block_table_batch_stride;
+        k.page = paged ? p->page_block_size : 1;
+        k.bt_rows = p->block_table_rows;
+        k.num_blocks = paged ? p->batch_cache : 0;
+        k.batch_cache = p->batch_cache;
+        k.kv_capacity = pl.kv_capacity;
+        k.cos = p->rotary_cos;
+        k.sin = p->rotary_sin;
+        k.cs_stride = p->rotary_dim / 2;
+        k.rotary_dim = pl.rotary ? p->rotary_dim : 0;
+        k.interleaved = p->rotary_interleaved;
+        k.seqlen_ro = p->seqlen_ro;
+        k.q = p->q;
+        k.q_sb = p->q_batch_stride;
+        k.q_si = p->q_row_stride;
+        k.q_sh = p->q_head_stride;
+        k.q_out = pl.rotary ? ws + pl.off_qrot : nullptr;
+        const bool local = p->window_size_left >= 0 || p->window_size_right >= 0;
+        k.q_same_pos = !(p->is_causal || local);
+        k.B = p->batch;
+        k.S_new = p->seqlen_new;
+        k.Sq = p->seqlen_q;
+        k.H = p->nheads;
+        k.Hk = p->nheads_k;
+        k.D = p->headdim;
+        k.Dv = p->headdim_v;
+        hipError_t e = fa::launch_kv_prep(k, p->dtype, stream);
+        if (e != hipSuccess) return fail(FA_EHIP, "kv_prep launch failed: %s", hipGetErrorString(e));
+        if (pl.rotary) {
+            q_ptr = ws + pl.off_qrot;
+            q_sh = p->headdim;
+            q_si = (int64_t)p->nheads * p->headdim;
+            q_sb = (int64_t)p->seqlen_q * q_si;
+        }
+    }
+
+    fa::FwdArgs a{};
+    a.q = q_ptr;
+    a.q_sb = q_sb;
+    a.q_si = q_si;
+    a.q_sh = q_sh;
+    a.k = p->k;
+    a.k_sb = p->k_batch_stride;
+    a.k_si = p->k_row_stride;
+    a.k_sh = p->k_head_stride;
+    a.v = p->v;
+    a.v_sb = p->v_batch_stride;
+    a.v_si = p->v_row_stride;
+    a.v_sh = p->v_head_stride;
+    a.out = p->out;
+    a.o_sb = p->out_batch_stride;
+    a.o_si = p->out_row_stride;
+    a.o_sh = p->out_head_stride;
+    a.lse = p->softmax_lse;
+    if (kind == FA_KIND_VARLEN) {
+        a.lse_sb = 0;
+        a.lse_sh = p->total_q;
+    } else {
+        a.lse_sb = (int64_t)p->nheads * p->seqlen_q;
+        a.lse_sh = p->seqlen_q;
+    }
+    a.seqlens_k = kind == FA_KIND_DENSE ? nullptr : p->cache_seqlens;  // kvcache lengths / varlen seqused_k
+    a.cu_seqlens_q = kind == FA_KIND_VARLEN ? p->cu_seqlens_q : nullptr;
+    a.cu_seqlens_k = kind == FA_KIND_VARLEN ? p->cu_seqlens_k : nullptr;
+    a.block_table = p->block_table;
+    a.batch_idx = kind == FA_KIND_KVCACHE ? p->cache_batch_idx : nullptr;
+    a.alibi = p->alibi_slopes;
+    a.bt_stride = p->block_table_batch_stride;
+    a.alibi_sb = p->alibi_batch_stride;
+    a.scale = p->softmax_scale;
+    a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
+    a.softcap = p->softcap;
+    a.B = p->batch;
+    a.Sq = p->seqlen_q;
+    a.Sk = kind == FA_KIND_KVCACHE ? pl.kv_capacity : p->seqlen_k;
+    a.H = p->nheads;
+    a.Hk = p->nheads_k;
+    a.g = pl.g;
+    a.seqlen_new = (kind == FA_KIND_KVCACHE && p->k_new) ? p->seqlen_new : 0;
+    // window normalisation (flash_api.cpp:483-494): the seqlen-dependent rules
+    // leave the mask unchanged, causal forces the right edge to the diagonal
+    int wl = p->window_size_left < 0 ? -1 : p->window_size_left;
+    int wr = p->window_size_right < 0 ? -1 : p->window_size_right;
+    if (p->is_causal) wr = 0;
+    a.wl = wl;
+    a.wr = wr;
+    a.page = paged ? p->page_block_size : 1;
+    a.bt_rows = p->block_table_rows;
+    a.num_blocks = paged ? p->batch_cache : 0;
+    a.batch_cache = kind == FA_KIND_KVCACHE ? p->batch_cache : p->batch;
+    a.kv_capacity = pl.kv_capacity;
+    a.part_o = pl.allow_split ? reinterpret_cast<float*>(ws + pl.off_po) : nullptr;
+    a.part_lse = pl.allow_split ? reinterpret_cast<float*>(ws + pl.off_plse) : nullptr;
+    a.sched = reinterpret_cast<int*>(ws + pl.off_sched);
+    a.allow_split = pl.allow_split ? 1 : 0;
+    a.num_splits = p->num_splits > 1 ? p->num_splits : 0;
+    a.target_items = pl.target_items;
+    a.min_chunk = pl.min_chunk;
+
+    hipError_t e = fa::launch_fwd(a, p->dtype, p->headdim, pl.decode, pl.grid, stream);
+    if (e != hipSuccess) return fail(FA_EHIP, "attention launch failed: %s", hipGetErrorString(e));
+    if (pl.allow_split) {
+        fa::CombineArgs c{};
+        c.out = p->out;
+        c.o_sb = a.o_sb;
+        c.o_si = a.o_si;
+        c.o_sh = a.o_sh;
+        c.lse = a.lse;
+        c.lse_sb = a.lse_sb;
+        c.lse_sh = a.lse_sh;
+        c.part_o = a.part_o;
+        c.part_lse = a.part_lse;
+        c.sched = a.sched;
+        c.cu_seqlens_q = a.cu_seqlens_q;
+        c.B = p->batch;
+        c.Sq = p->seqlen_q;
+        c.H = p->nheads;
+        c.Hk = p->nheads_k;
+        c.g = pl.g;
+        c.BM = pl.BM;
+        c.mt_max = pl.mt_max;
+        int grid = (int)std::min<int64_t>((int64_t)p->batch * p->nheads_k * pl.mt_max, INT_MAX);
+        e = fa::launch_combine(c, p->dtype, p->headdim, grid, stream);
+        if (e != hipSuccess) return fail(FA_EHIP, "combine launch failed: %s", hipGetErrorString(e));
+    }
+    return FA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_abi_version(void) { return FA_MI355X_ABI_VERSION; }
+
+const char* fa_last_error(void) { return g_err.c_str(); }
+
+fa_status_t fa_validate(const fa_fwd_params* p, int32_t kind) { return validate(p, kind); }
+
+fa_status_t fa_fwd_workspace_size(const fa_fwd_params* p, int32_t kind, size_t* bytes) {
+    if (!bytes) return fail(FA_EINVAL, "bytes must not be null");
+    fa_status_t st = validate(p, kind);
+    if (st != FA_OK) return st;
+    Plan pl;
+    make_plan(p, kind, pl);
+    *bytes = pl.total;
+    return FA_OK;
+}
+
+fa_status_t fa_mha_fwd_kvcache(const fa_fwd_params* p, void* stream) { return run_forward(p, FA_KIND_KVCACHE, stream); }
+
+fa_status_t fa_mha_fwd(const fa_fwd_params* p, void* stream) { return run_forward(p, FA_KIND_DENSE, stream); }
+
+fa_status_t fa_mha_varlen_fwd(const fa_fwd_params* p, void* stream) { return run_forward(p, FA_KIND_VARLEN, stream); }
+
+fa_status_t fa_combine(const float* out_partial, const float* lse_partial, int32_t num_splits, int64_t rows,
+                       int32_t headdim_v, void* out, int64_t out_row_stride, int32_t out_dtype, float* lse,
+                       void* stream) {
+    if (!out_partial || !lse_partial || !out) return fail(FA_EINVAL, "out_partial, lse_partial and out are required");
+    if (num_splits < 1 || rows < 0) return fail(FA_EINVAL, "num_splits must be >= 1 and rows >= 0");
+    if (headdim_v < 4 || headdim_v % 4) return fail(FA_EINVAL, "headdim_v must be a positive multiple of 4");
+    if (out_dtype != FA_DTYPE_FP16 && out_dtype != FA_DTYPE_BF16 && out_dtype != FA_DTYPE_FP32)
+        return fail(FA_EINVAL, "out_dtype must be fp16, bf16 or fp32");
+    if (out_row_stride < headdim_v || out_row_stride % 4)
+        return fail(FA_EINVAL, "out_row_stride must be >= headdim_v and a multiple of 4");
+    if (!aligned16(out_partial) || !aligned16(out)) return fail(FA_EINVAL, "out_partial and out must be 16-byte aligned");
+    if (rows == 0) return FA_OK;
+    hipError_t e = fa::launch_combine_flat(out_partial, lse_partial, num_splits, rows, headdim_v, out, out_row_stride,
+                                           out_dtype, lse, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(FA_EHIP, "combine launch failed: %s", hipGetErrorString(e));
+    return FA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,81 @@
+// fa_common.h -- device-side types and helpers shared by the gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+enum : int { DT_FP16 = 0, DT_BF16 = 1 };
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// 16x16x32 MFMA on 16-byte packed operands. Lane l holds A[l%16][8*(l/16)+e]
+// and B[8*(l/16)+e][l%16]; the result lane l holds D[4*(l/16)+i][l%16].
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+    if constexpr (DT == DT_BF16) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+}
+
+// Round-to-nearest-even conversions of 8 floats into one 16-byte operand.
+template <int DT>
+__device__ __forceinline__ u32x4 pack8(f32x8 v) {
+    if constexpr (DT == DT_BF16) {
+        bf16x8 h = __builtin_convertvector(v, bf16x8);
+        return __builtin_bit_cast(u32x4, h);
+    } else {
+        f16x8 h = __builtin_convertvector(v, f16x8);
+        return __builtin_bit_cast(u32x4, h);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ uint16_t f32_to_16(float f) {
+    if constexpr (DT == DT_BF16) {
+        return __builtin_bit_cast(uint16_t, (__bf16)f);
+    } else {
+        return __builtin_bit_cast(uint16_t, (_Float16)f);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ float f16_to_32(uint16_t h) {
+    if constexpr (DT == DT_BF16) {
+        return __builtin_bit_cast(float, (uint32_t)h << 16);
+    } else {
+        return (float)__builtin_bit_cast(_Float16, h);
+    }
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+__device__ __forceinline__ float wave_max16x4(float v) {
+    // max over the 4 lanes l, l^16, l^32, l^48 that hold the same MFMA column
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum16x4(float v) {
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+}  // namespace fa

@@ -1,0 +1,98 @@
+// fa_kernel_args.h -- the by-value kernel argument blocks (host and device).
+//
+// Every launch receives one of these structs as its only argument, so the
+// host never copies tiling data to the device and never reads device memory
+// (the reference copies a tiling struct and a 4 MiB mask H2D and reads
+// cache_seqlens back D2H on every call: flash_api.cpp:459,575-580 of
+// csrc/arch22/flash_attn_npu_v2).
+#pragma once
+#include <stdint.h>
+
+namespace fa {
+
+// Strides are in elements; the head dimension is contiguous.
+struct FwdArgs {
+    const void* q;
+    int64_t q_sb, q_si, q_sh;
+    const void* k;
+    int64_t k_sb, k_si, k_sh;
+    const void* v;
+    int64_t v_sb, v_si, v_sh;
+    void* out;
+    int64_t o_sb, o_si, o_sh;
+    float* lse;
+    int64_t lse_sb, lse_sh;  // (B,H,Sq): b*lse_sb + h*lse_sh + i; varlen (H,T): h*lse_sh + cu_q[b] + i
+
+    const int* seqlens_k;  // per-batch cached length (kvcache), may be null
+    const int* cu_seqlens_q;
+    const int* cu_seqlens_k;
+    const int* block_table;
+    const int* batch_idx;
+    const float* alibi;
+    int64_t bt_stride;
+    int64_t alibi_sb;
+
+    float scale;        // softmax_scale
+    float scale_log2;   // softmax_scale * log2(e)
+    float softcap;      // 0 = off
+
+    int B, Sq, Sk, H, Hk, g;
+    int seqlen_new;     // tokens appended this call (added to seqlens_k)
+    int wl, wr;         // normalised window, -1 = unbounded, causal => wr = 0
+    int page;           // paged: tokens per block
+    int bt_rows;        // paged: rows of the block table (clamp bound)
+    int num_blocks;     // paged: rows of the block pool (clamp bound)
+    int batch_cache;    // contiguous: rows of the cache (clamp bound for batch_idx)
+    int kv_capacity;    // keys addressable per sequence
+
+    // split-KV
+    float* part_o;      // [item][BM][Dv] fp32
+    float* part_lse;    // [item][BM]
+    int* sched;         // [0..B]: item prefix, [B+1..2B]: splits per batch
+    int allow_split;
+    int num_splits;     // > 0: forced split count
+    int target_items;   // auto split: aim for about this many work items
+    int min_chunk;      // auto split: smallest chunk of keys per item
+};
+
+struct CombineArgs {
+    void* out;
+    int64_t o_sb, o_si, o_sh;
+    float* lse;
+    int64_t lse_sb, lse_sh;
+    const float* part_o;
+    const float* part_lse;
+    const int* sched;
+    const int* cu_seqlens_q;
+    int B, Sq, H, Hk, g, BM, mt_max;
+};
+
+struct KvPrepArgs {
+    // new tokens (B, S_new, Hk, D) / (B, S_new, Hk, Dv)
+    const void* k_new;
+    int64_t kn_sb, kn_si, kn_sh;
+    const void* v_new;
+    int64_t vn_sb, vn_si, vn_sh;
+    void* k_cache;
+    int64_t k_sb, k_si, k_sh;
+    void* v_cache;
+    int64_t v_sb, v_si, v_sh;
+    const int* seqlens;
+    const int* batch_idx;
+    const int* block_table;
+    int64_t bt_stride;
+    int page, num_blocks, batch_cache, kv_capacity, bt_rows;
+    // rotary (cos/sin: (seqlen_ro, rotary_dim/2))
+    const void* cos;
+    const void* sin;
+    int64_t cs_stride;
+    int rotary_dim, interleaved, seqlen_ro;
+    // q rotation: q (B, Sq, H, D) -> q_out (B, Sq, H, D) contiguous
+    const void* q;
+    int64_t q_sb, q_si, q_sh;
+    void* q_out;
+    int q_same_pos;
+    int B, S_new, Sq, H, Hk, D, Dv;
+};
+
+}  // namespace fa

@@ -1,0 +1,398 @@
+// fa_torch_ops.cpp -- PyTorch-ROCm operators over the C ABI (libfa_mi355x.so).
+//
+// Registers torch.ops.fa_mi355x.{fwd_kvcache, fwd, varlen_fwd, fwd_combine}.
+// Argument order and meaning follow the reference pybind entry points
+// (csrc/arch22/flash_attn_npu_v2/flash_api.cpp: mha_fwd_kvcache :356-377,
+// mha_fwd :628-640, mha_varlen_fwd :828-850, bound at :1301-1309). Unlike the
+// reference op (flash_attn_npu_v3/interface_arch22.py:63, mutates_args=()),
+// the kvcache op declares that it writes k_cache / v_cache.
+//
+// This layer only converts tensors to fa_fwd_params, allocates outputs and
+// the workspace from the caching allocator, and picks the current HIP stream.
+// Errors from the library surface as RuntimeError with the library's message.
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <cmath>
+#include <optional>
+
+#include "../../../include/fa_mi355x.h"
+
+namespace {
+
+using at::Tensor;
+using OptT = std::optional<Tensor>;
+
+int32_t dtype_code(const Tensor& t) {
+    if (t.scalar_type() == at::kHalf) return FA_DTYPE_FP16;
+    if (t.scalar_type() == at::kBFloat16) return FA_DTYPE_BF16;
+    TORCH_CHECK(false, "FlashAttention only support fp16 and bf16 data type");
+}
+
+void check_status(fa_status_t st) { TORCH_CHECK(st == FA_OK, "fa_mi355x: ", fa_last_error()); }
+
+void check_dev(const Tensor& t, const Tensor& q, const char* name) {
+    TORCH_CHECK(t.is_cuda(), name, " must be on a GPU device");
+    TORCH_CHECK(t.device() == q.device(), name, " must be on the same device as q");
+}
+
+const int32_t* i32_ptr(const OptT& t, const Tensor& q, const char* name) {
+    if (!t.has_value()) return nullptr;
+    check_dev(*t, q, name);
+    TORCH_CHECK(t->scalar_type() == at::kInt, name, " must have dtype int32");
+    TORCH_CHECK(t->stride(-1) == 1, name, " must have contiguous last dimension");
+    return t->data_ptr<int32_t>();
+}
+
+Tensor workspace_for(const fa_fwd_params& p, int32_t kind, const Tensor& q) {
+    size_t bytes = 0;
+    check_status(fa_fwd_workspace_size(&p, kind, &bytes));
+    return at::empty({(int64_t)std::max<size_t>(bytes, 256)}, q.options().dtype(at::kByte));
+}
+
+void* cur_stream() { return (void*)c10::hip::getCurrentHIPStream().stream(); }
+
+void set_window(fa_fwd_params& p, bool is_causal, int64_t wl, int64_t wr) {
+    p.is_causal = is_causal ? 1 : 0;
+    p.window_size_left = (int32_t)wl;
+    p.window_size_right = (int32_t)wr;
+}
+
+void set_alibi(fa_fwd_params& p, const OptT& alibi, const Tensor& q, int64_t batch, int64_t nheads) {
+    if (!alibi.has_value()) return;
+    check_dev(*alibi, q, "alibi_slopes");
+    TORCH_CHECK(alibi->scalar_type() == at::kFloat, "ALiBi slopes must have dtype fp32");
+    TORCH_CHECK(alibi->stride(-1) == 1, "ALiBi slopes tensor must have contiguous last dimension");
+    TORCH_CHECK(alibi->sizes() == at::IntArrayRef({nheads}) || alibi->sizes() == at::IntArrayRef({batch, nheads}),
+                "alibi_slopes must have shape (nheads) or (batch_size, nheads)");
+    p.alibi_slopes = alibi->data_ptr<float>();
+    p.alibi_batch_stride = alibi->dim() == 2 ? alibi->stride(0) : 0;
+}
+
+// ---- flash_attn_with_kvcache -----------------------------------------------------------
+std::tuple<Tensor, Tensor> fwd_kvcache(const Tensor& q, Tensor& kcache, Tensor& vcache, const OptT& k_new,
+                                       const OptT& v_new, const OptT& seqlens_k, const OptT& rotary_cos,
+                                       const OptT& rotary_sin, const OptT& cache_batch_idx, const OptT& leftpad_k,
+                                       const OptT& block_table, const OptT& alibi_slopes, double softmax_scale,
+                                       bool is_causal, int64_t window_size_left, int64_t window_size_right,
+                                       double softcap, bool is_rotary_interleaved, int64_t num_splits) {
+    c10::DeviceGuard guard(q.device());
+    TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
+    check_dev(kcache, q, "k_cache");
+    check_dev(vcache, q, "v_cache");
+    const int32_t dt = dtype_code(q);
+    TORCH_CHECK(kcache.scalar_type() == q.scalar_type() && vcache.scalar_type() == q.scalar_type(),
+                "query and key/value must have the same dtype");
+    TORCH_CHECK(q.dim() == 4, "q must have shape (batch_size, seqlen_q, num_heads, head_size)");
+    TORCH_CHECK(kcache.dim() == 4 && vcache.dim() == 4, "k_cache/v_cache must be 4-dimensional");
+    TORCH_CHECK(q.stride(-1) == 1 && kcache.stride(-1) == 1 && vcache.stride(-1) == 1,
+                "Input tensor must have contiguous last dimension");
+    TORCH_CHECK(!leftpad_k.has_value(), "cache_leftpad is not supported");
+    const bool paged = block_table.has_value();
+    fa_fwd_params p{};
+    p.abi_version = FA_MI355X_ABI_VERSION;
+    p.dtype = dt;
+    p.batch = (int32_t)q.size(0);
+    p.seqlen_q = (int32_t)q.size(1);
+    p.nheads = (int32_t)q.size(2);
+    p.headdim = (int32_t)q.size(3);
+    p.nheads_k = (int32_t)kcache.size(2);
+    p.headdim_v = (int32_t)vcache.size(3);
+    TORCH_CHECK(kcache.size(3) == p.headdim, "k_cache head size must match q");
+    TORCH_CHECK(vcache.sizes() == kcache.sizes(), "v_cache must have the same shape as k_cache");
+    p.batch_cache = (int32_t)kcache.size(0);
+    p.seqlen_k = (int32_t)kcache.size(1);
+    p.q = q.data_ptr();
+    p.q_batch_stride = q.stride(0);
+    p.q_row_stride = q.stride(1);
+    p.q_head_stride = q.stride(2);
+    p.k = kcache.data_ptr();
+    p.k_batch_stride = kcache.stride(0);
+    p.k_row_stride = kcache.stride(1);
+    p.k_head_stride = kcache.stride(2);
+    p.v = vcache.data_ptr();
+    p.v_batch_stride = vcache.stride(0);
+    p.v_row_stride = vcache.stride(1);
+    p.v_head_stride = vcache.stride(2);
+    if (paged) {
+        p.block_table = i32_ptr(block_table, q, "block_table");
+        TORCH_CHECK(block_table->dim() == 2, "block_table must be 2-dimensional");
+        p.block_table_batch_stride = block_table->stride(0);
+        p.max_blocks_per_seq = (int32_t)block_table->size(1);
+        p.block_table_rows = (int32_t)block_table->size(0);
+        p.page_block_size = (int32_t)kcache.size(1);
+        const int64_t rows_needed = cache_batch_idx.has_value() ? 1 : q.size(0);
+        TORCH_CHECK(block_table->size(0) >= rows_needed, "block_table must have a row per batch entry");
+    }
+    Tensor kn, vn;
+    if (k_new.has_value()) {
+        TORCH_CHECK(v_new.has_value(), "If key is supplied, value must also be passed in");
+        TORCH_CHECK(seqlens_k.has_value(), "If key is supplied, seqlens_k must also be passed in");
+        kn = k_new->stride(-1) == 1 ? *k_new : k_new->contiguous();
+        vn = v_new->stride(-1) == 1 ? *v_new : v_new->contiguous();
+        check_dev(kn, q, "k");
+        check_dev(vn, q, "v");
+        TORCH_CHECK(kn.scalar_type() == q.scalar_type() && vn.scalar_type() == q.scalar_type(),
+                    "Key and value must have the same dtype as query");
+        TORCH_CHECK(kn.dim() == 4 && kn.size(0) == q.size(0) && kn.size(2) == p.nheads_k && kn.size(3) == p.headdim,
+                    "k must have shape (batch_size, seqlen_new, num_heads_k, head_size)");
+        TORCH_CHECK(vn.sizes() == kn.sizes(), "v must have the same shape as k");
+        p.k_new = kn.data_ptr();
+        p.knew_batch_stride = kn.stride(0);
+        p.knew_row_stride = kn.stride(1);
+        p.knew_head_stride = kn.stride(2);
+        p.v_new = vn.data_ptr();
+        p.vnew_batch_stride = vn.stride(0);
+        p.vnew_row_stride = vn.stride(1);
+        p.vnew_head_stride = vn.stride(2);
+        p.seqlen_new = (int32_t)kn.size(1);
+    } else {
+        TORCH_CHECK(!v_new.has_value(), "If value is supplied, key must also be passed in");
+    }
+    if (seqlens_k.has_value()) {
+        p.cache_seqlens = i32_ptr(seqlens_k, q, "seqlens_k");
+        TORCH_CHECK(seqlens_k->numel() == q.size(0), "seqlens_k must have shape (batch_size)");
+    }
+    if (cache_batch_idx.has_value()) {
+        p.cache_batch_idx = i32_ptr(cache_batch_idx, q, "cache_batch_idx");
+        TORCH_CHECK(cache_batch_idx->numel() == q.size(0), "cache_batch_idx must have shape (batch_size)");
+    }
+    if (rotary_cos.has_value()) {
+        TORCH_CHECK(rotary_sin.has_value(), "rotary_sin must be given with rotary_cos");
+        check_dev(*rotary_cos, q, "rotary_cos");
+        check_dev(*rotary_sin, q, "rotary_sin");
+        TORCH_CHECK(rotary_cos->scalar_type() == q.scalar_type() && rotary_sin->scalar_type() == q.scalar_type(),
+                    "rotary_cos/sin must have the same dtype as query");
+        TORCH_CHECK(rotary_cos->dim() == 2 && rotary_cos->sizes() == rotary_sin->sizes(),
+                    "rotary_cos/sin must have shape (seqlen_ro, rotary_dim / 2)");
+        TORCH_CHECK(rotary_cos->is_contiguous() && rotary_sin->is_contiguous(), "rotary_cos/sin must be contiguous");
+        p.rotary_cos = rotary_cos->data_ptr();
+        p.rotary_sin = rotary_sin->data_ptr();
+        p.rotary_dim = (int32_t)rotary_cos->size(1) * 2;
+        p.seqlen_ro = (int32_t)rotary_cos->size(0);
+        p.rotary_interleaved = is_rotary_interleaved ? 1 : 0;
+    }
+    set_alibi(p, alibi_slopes, q, q.size(0), q.size(2));
+    p.softmax_scale = (float)softmax_scale;
+    p.softcap = (float)softcap;
+    set_window(p, is_causal, window_size_left, window_size_right);
+    p.num_splits = (int32_t)num_splits;
+    Tensor out = at::empty(q.sizes(), q.options());
+    Tensor lse = at::empty({q.size(0), q.size(2), q.size(1)}, q.options().dtype(at::kFloat));
+    p.out = out.data_ptr();
+    p.out_batch_stride = out.stride(0);
+    p.out_row_stride = out.stride(1);
+    p.out_head_stride = out.stride(2);
+    p.softmax_lse = lse.data_ptr<float>();
+    Tensor ws = workspace_for(p, FA_KIND_KVCACHE, q);
+    p.workspace = ws.data_ptr();
+    p.workspace_bytes = (size_t)ws.numel();
+    check_status(fa_mha_fwd_kvcache(&p, cur_stream()));
+    return {out, lse};
+}
+
+// ---- flash_attn_func ------------------------------------------------------------------------
+std::tuple<Tensor, Tensor> fwd(const Tensor& q, const Tensor& k, const Tensor& v, const OptT& alibi_slopes,
+                               double p_dropout, double softmax_scale, bool is_causal, int64_t window_size_left,
+                               int64_t window_size_right, double softcap) {
+    c10::DeviceGuard guard(q.device());
+    TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
+    check_dev(k, q, "k");
+    check_dev(v, q, "v");
+    const int32_t dt = dtype_code(q);
+    TORCH_CHECK(k.scalar_type() == q.scalar_type() && v.scalar_type() == q.scalar_type(),
+                "query and key/value must have the same dtype");
+    TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "q, k, v must be 4-dimensional (batch, seqlen, heads, dim)");
+    TORCH_CHECK(q.stride(-1) == 1 && k.stride(-1) == 1 && v.stride(-1) == 1,
+                "Input tensor must have contiguous last dimension");
+    TORCH_CHECK(k.size(0) == q.size(0) && v.sizes() == k.sizes(), "k and v must have shape (batch_size, seqlen_k, num_heads_k, head_size)");
+    TORCH_CHECK(k.size(3) == q.size(3), "k head size must match q");
+    fa_fwd_params p{};
+    p.abi_version = FA_MI355X_ABI_VERSION;
+    p.dtype = dt;
+    p.batch = (int32_t)q.size(0);
+    p.seqlen_q = (int32_t)q.size(1);
+    p.nheads = (int32_t)q.size(2);
+    p.headdim = (int32_t)q.size(3);
+    p.nheads_k = (int32_t)k.size(2);
+    p.headdim_v = (int32_t)v.size(3);
+    p.seqlen_k = (int32_t)k.size(1);
+    p.batch_cache = p.batch;
+    p.q = q.data_ptr();
+    p.q_batch_stride = q.stride(0);
+    p.q_row_stride = q.stride(1);
+    p.q_head_stride = q.stride(2);
+    p.k = const_cast<void*>(k.data_ptr());
+    p.k_batch_stride = k.stride(0);
+    p.k_row_stride = k.stride(1);
+    p.k_head_stride = k.stride(2);
+    p.v = const_cast<void*>(v.data_ptr());
+    p.v_batch_stride = v.stride(0);
+    p.v_row_stride = v.stride(1);
+    p.v_head_stride = v.stride(2);
+    set_alibi(p, alibi_slopes, q, q.size(0), q.size(2));
+    p.dropout_p = (float)p_dropout;
+    p.softmax_scale = (float)softmax_scale;
+    p.softcap = (float)softcap;
+    set_window(p, is_causal, window_size_left, window_size_right);
+    p.num_splits = 0;
+    Tensor out = at::empty(q.sizes(), q.options());
+    Tensor lse = at::empty({q.size(0), q.size(2), q.size(1)}, q.options().dtype(at::kFloat));
+    p.out = out.data_ptr();
+    p.out_batch_stride = out.stride(0);
+    p.out_row_stride = out.stride(1);
+    p.out_head_stride = out.stride(2);
+    p.softmax_lse = lse.data_ptr<float>();
+    Tensor ws = workspace_for(p, FA_KIND_DENSE, q);
+    p.workspace = ws.data_ptr();
+    p.workspace_bytes = (size_t)ws.numel();
+    check_status(fa_mha_fwd(&p, cur_stream()));
+    return {out, lse};
+}
+
+// ---- flash_attn_varlen_func -----------------------------------------------------------------------
+std::tuple<Tensor, Tensor> varlen_fwd(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& cu_seqlens_q,
+                                      const OptT& cu_seqlens_k, const OptT& seqused_k, const OptT& block_table,
+                                      const OptT& alibi_slopes,
+                                      int64_t max_seqlen_q, int64_t max_seqlen_k, double p_dropout,
+                                      double softmax_scale, bool is_causal, int64_t window_size_left,
+                                      int64_t window_size_right, double softcap) {
+    c10::DeviceGuard guard(q.device());
+    TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
+    check_dev(k, q, "k");
+    check_dev(v, q, "v");
+    const int32_t dt = dtype_code(q);
+    TORCH_CHECK(k.scalar_type() == q.scalar_type() && v.scalar_type() == q.scalar_type(),
+                "query and key/value must have the same dtype");
+    TORCH_CHECK(q.dim() == 3, "q must have shape (total_q, num_heads, head_size)");
+    TORCH_CHECK(q.stride(-1) == 1 && k.stride(-1) == 1 && v.stride(-1) == 1,
+                "Input tensor must have contiguous last dimension");
+    const bool paged = block_table.has_value();
+    fa_fwd_params p{};
+    p.abi_version = FA_MI355X_ABI_VERSION;
+    p.dtype = dt;
+    p.batch = (int32_t)(cu_seqlens_q.numel() - 1);
+    TORCH_CHECK(!cu_seqlens_k.has_value() || cu_seqlens_k->numel() == cu_seqlens_q.numel(),
+                "cu_seqlens_q and cu_seqlens_k must have the same length");
+    TORCH_CHECK(!seqused_k.has_value() || seqused_k->numel() == p.batch, "seqused_k must have shape (batch_size)");
+    p.seqlen_q = (int32_t)max_seqlen_q;
+    p.total_q = (int32_t)q.size(0);
+    p.nheads = (int32_t)q.size(1);
+    p.headdim = (int32_t)q.size(2);
+    p.q = q.data_ptr();
+    p.q_batch_stride = 0;
+    p.q_row_stride = q.stride(0);
+    p.q_head_stride = q.stride(1);
+    if (paged) {
+        TORCH_CHECK(k.dim() == 4, "paged k must have shape (num_blocks, page_block_size, num_heads_k, head_size)");
+        p.nheads_k = (int32_t)k.size(2);
+        p.headdim_v = (int32_t)v.size(3);
+        p.k_batch_stride = k.stride(0);
+        p.k_row_stride = k.stride(1);
+        p.k_head_stride = k.stride(2);
+        p.v_batch_stride = v.stride(0);
+        p.v_row_stride = v.stride(1);
+        p.v_head_stride = v.stride(2);
+        p.block_table = i32_ptr(block_table, q, "block_table");
+        p.block_table_batch_stride = block_table->stride(0);
+        p.max_blocks_per_seq = (int32_t)block_table->size(1);
+        p.block_table_rows = (int32_t)block_table->size(0);
+        p.page_block_size = (int32_t)k.size(1);
+        p.batch_cache = (int32_t)k.size(0);
+    } else {
+        TORCH_CHECK(k.dim() == 3, "k must have shape (total_k, num_heads_k, head_size)");
+        p.nheads_k = (int32_t)k.size(1);
+        p.headdim_v = (int32_t)v.size(2);
+        p.k_batch_stride = 0;
+        p.k_row_stride = k.stride(0);
+        p.k_head_stride = k.stride(1);
+        p.v_batch_stride = 0;
+        p.v_row_stride = v.stride(0);
+        p.v_head_stride = v.stride(1);
+        p.batch_cache = p.batch;
+    }
+    p.seqlen_k = (int32_t)max_seqlen_k;
+    p.k = const_cast<void*>(k.data_ptr());
+    p.v = const_cast<void*>(v.data_ptr());
+    p.cu_seqlens_q = i32_ptr(cu_seqlens_q, q, "cu_seqlens_q");
+    p.cu_seqlens_k = i32_ptr(cu_seqlens_k, q, "cu_seqlens_k");
+    p.cache_seqlens = i32_ptr(seqused_k, q, "seqused_k");
+    set_alibi(p, alibi_slopes, q, p.batch, q.size(1));
+    p.dropout_p = (float)p_dropout;
+    p.softmax_scale = (float)softmax_scale;
+    p.softcap = (float)softcap;
+    set_window(p, is_causal, window_size_left, window_size_right);
+    p.num_splits = 0;
+    Tensor out = at::empty(q.sizes(), q.options());
+    Tensor lse = at::empty({q.size(1), q.size(0)}, q.options().dtype(at::kFloat));
+    p.out = out.data_ptr();
+    p.out_batch_stride = 0;
+    p.out_row_stride = out.stride(0);
+    p.out_head_stride = out.stride(1);
+    p.softmax_lse = lse.data_ptr<float>();
+    Tensor ws = workspace_for(p, FA_KIND_VARLEN, q);
+    p.workspace = ws.data_ptr();
+    p.workspace_bytes = (size_t)ws.numel();
+    check_status(fa_mha_varlen_fwd(&p, cur_stream()));
+    return {out, lse};
+}
+
+// ---- flash_attn_combine --------------------------------------------------------------------------
+std::tuple<Tensor, Tensor> fwd_combine(const Tensor& out_partial, const Tensor& lse_partial, const OptT& out_,
+                                       std::optional<at::ScalarType> out_dtype) {
+    c10::DeviceGuard guard(out_partial.device());
+    TORCH_CHECK(out_partial.is_cuda() && lse_partial.is_cuda(), "inputs must be on a GPU device");
+    TORCH_CHECK(out_partial.scalar_type() == at::kFloat && lse_partial.scalar_type() == at::kFloat,
+                "out_partial and lse_partial must be fp32");
+    // out_partial (num_splits, ..., headdim_v); lse_partial (num_splits, ...)
+    TORCH_CHECK(out_partial.dim() >= 2 && lse_partial.dim() == out_partial.dim() - 1,
+                "lse_partial must have the shape of out_partial without its last dimension");
+    for (int64_t d = 0; d < lse_partial.dim(); ++d)
+        TORCH_CHECK(lse_partial.size(d) == out_partial.size(d), "lse_partial shape mismatch at dim ", d);
+    Tensor po = out_partial.contiguous();
+    Tensor pl = lse_partial.contiguous();
+    const int64_t S = po.size(0);
+    const int64_t Dv = po.size(-1);
+    const int64_t R = S > 0 ? po.numel() / (S * Dv) : 0;
+    at::ScalarType odt = out_dtype.has_value() ? *out_dtype : at::kFloat;
+    std::vector<int64_t> oshape(po.sizes().begin() + 1, po.sizes().end());
+    Tensor out = out_.has_value() ? *out_ : at::empty(oshape, po.options().dtype(odt));
+    TORCH_CHECK(out.is_contiguous() && out.numel() == R * Dv, "out must be contiguous with ", R * Dv, " elements");
+    int32_t code = out.scalar_type() == at::kFloat ? FA_DTYPE_FP32
+                   : out.scalar_type() == at::kBFloat16 ? FA_DTYPE_BF16
+                   : out.scalar_type() == at::kHalf ? FA_DTYPE_FP16 : -1;
+    TORCH_CHECK(code >= 0, "out dtype must be fp32, bf16 or fp16");
+    std::vector<int64_t> lshape(pl.sizes().begin() + 1, pl.sizes().end());
+    Tensor lse = at::empty(lshape, po.options());
+    check_status(fa_combine(po.data_ptr<float>(), pl.data_ptr<float>(), (int32_t)S, R, (int32_t)Dv, out.data_ptr(), Dv,
+                            code, lse.data_ptr<float>(), cur_stream()));
+    return {out, lse};
+}
+
+}  // namespace
+
+TORCH_LIBRARY(fa_mi355x, m) {
+    m.def(
+        "fwd_kvcache(Tensor q, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor? k, Tensor? v, Tensor? seqlens_k, "
+        "Tensor? rotary_cos, Tensor? rotary_sin, Tensor? cache_batch_idx, Tensor? leftpad_k, Tensor? block_table, "
+        "Tensor? alibi_slopes, float softmax_scale, bool is_causal, int window_size_left, int window_size_right, "
+        "float softcap, bool is_rotary_interleaved, int num_splits) -> (Tensor, Tensor)");
+    m.def(
+        "fwd(Tensor q, Tensor k, Tensor v, Tensor? alibi_slopes, float p_dropout, float softmax_scale, bool is_causal, "
+        "int window_size_left, int window_size_right, float softcap) -> (Tensor, Tensor)");
+    m.def(
+        "varlen_fwd(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor? cu_seqlens_k, Tensor? seqused_k, "
+        "Tensor? block_table, "
+        "Tensor? alibi_slopes, int max_seqlen_q, int max_seqlen_k, float p_dropout, float softmax_scale, "
+        "bool is_causal, int window_size_left, int window_size_right, float softcap) -> (Tensor, Tensor)");
+    m.def("fwd_combine(Tensor out_partial, Tensor lse_partial, Tensor? out, ScalarType? out_dtype) -> (Tensor, Tensor)");
+}
+
+TORCH_LIBRARY_IMPL(fa_mi355x, CUDA, m) {
+    m.impl("fwd_kvcache", &fwd_kvcache);
+    m.impl("fwd", &fwd);
+    m.impl("varlen_fwd", &varlen_fwd);
+    m.impl("fwd_combine", &fwd_combine);
+}

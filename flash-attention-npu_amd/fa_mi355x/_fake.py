@@ -1,0 +1,35 @@
+"""Meta (fake) implementations of the fa_mi355x operators, so the ops trace
+under torch.compile. Output shapes follow the reference fakes
+(flash_attn_npu_v3/interface_arch22.py:157-259, flash_attn_npu_v2/
+interface_arch22.py:79-106,178-199): out like q, LSE (B, H, Sq) fp32, or
+(H, total_q) for the varlen layout."""
+import torch
+
+
+@torch.library.register_fake("fa_mi355x::fwd_kvcache")
+def _fwd_kvcache_fake(q, k_cache, v_cache, k, v, seqlens_k, rotary_cos, rotary_sin, cache_batch_idx, leftpad_k,
+                      block_table, alibi_slopes, softmax_scale, is_causal, window_size_left, window_size_right,
+                      softcap, is_rotary_interleaved, num_splits):
+    b, sq, h, _ = q.shape
+    return torch.empty_like(q), q.new_empty((b, h, sq), dtype=torch.float32)
+
+
+@torch.library.register_fake("fa_mi355x::fwd")
+def _fwd_fake(q, k, v, alibi_slopes, p_dropout, softmax_scale, is_causal, window_size_left, window_size_right,
+              softcap):
+    b, sq, h, _ = q.shape
+    return torch.empty_like(q), q.new_empty((b, h, sq), dtype=torch.float32)
+
+
+@torch.library.register_fake("fa_mi355x::varlen_fwd")
+def _varlen_fwd_fake(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, block_table, alibi_slopes, max_seqlen_q, max_seqlen_k,
+                     p_dropout, softmax_scale, is_causal, window_size_left, window_size_right, softcap):
+    t, h, _ = q.shape
+    return torch.empty_like(q), q.new_empty((h, t), dtype=torch.float32)
+
+
+@torch.library.register_fake("fa_mi355x::fwd_combine")
+def _fwd_combine_fake(out_partial, lse_partial, out, out_dtype):
+    dt = out_dtype if out_dtype is not None else torch.float32
+    o = out if out is not None else out_partial.new_empty(out_partial.shape[1:], dtype=dt)
+    return o, lse_partial.new_empty(lse_partial.shape[1:])

@@ -1,0 +1,154 @@
+/*
+ * fa_mi355x.h -- C ABI of the MI355X (gfx950) FlashAttention forward library
+ * (libfa_mi355x.so). Plain pointers, sizes and a stream handle: no torch or
+ * HIP types, so any FFI (ctypes, cgo, JNI, N-API) can bind it.
+ *
+ * The entry points replace the reference's pybind11 forward functions
+ * (paths relative to the reference repository):
+ *   fa_mha_fwd_kvcache  <- mha_fwd_kvcache  csrc/arch22/flash_attn_npu_v2/flash_api.cpp:356-626
+ *                          (bound as fwd_kvcache at flash_api.cpp:1306) and the kvcache branch of
+ *                          mha_fwd           csrc/arch22/flash_attn_npu_v3/flash_api.cpp:60-491
+ *   fa_mha_fwd          <- mha_fwd          csrc/arch22/flash_attn_npu_v2/flash_api.cpp:628-826
+ *                          (bound as fwd at flash_api.cpp:1303)
+ *   fa_mha_varlen_fwd   <- mha_varlen_fwd   csrc/arch22/flash_attn_npu_v2/flash_api.cpp:828-1060
+ *                          (bound as varlen_fwd at flash_api.cpp:1304)
+ *   fa_fwd_workspace_size / fa_validate
+ *                       <- the host-side validation and workspace sizing inside those
+ *                          functions (flash_api.cpp:382-441 and :541-565)
+ *   fa_combine          <- CombineScale (csrc/arch22/flash_attn_npu_v2/CombineScale.hpp:76-357),
+ *                          exposed as the v3 flash_attn_combine
+ *                          (flash_attn_npu_v3/interface_arch22.py:930-931)
+ *
+ * Conventions
+ *   - All tensor strides are in ELEMENTS; the last (head) dimension must be
+ *     contiguous and every row start 16-byte aligned.
+ *   - The library never allocates or frees device memory. The caller passes a
+ *     workspace of at least fa_fwd_workspace_size() bytes (256-byte aligned).
+ *   - Every function returns FA_OK or an error code; fa_last_error() gives a
+ *     thread-local message for the last failure on the calling thread.
+ *   - Work is enqueued on `stream` (a hipStream_t, or NULL for the null
+ *     stream). Nothing synchronises the host and nothing reads device memory
+ *     on the host.
+ */
+#ifndef FA_MI355X_H
+#define FA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_MI355X_ABI_VERSION 1
+
+typedef enum {
+    FA_OK = 0,
+    FA_EINVAL = 1,        /* invalid argument (shape, stride, value) */
+    FA_EUNSUPPORTED = 2,  /* valid but not implemented (e.g. dropout) */
+    FA_EHIP = 3,          /* HIP runtime error at launch */
+    FA_EWORKSPACE = 4     /* workspace missing or too small */
+} fa_status_t;
+
+typedef enum { FA_DTYPE_FP16 = 0, FA_DTYPE_BF16 = 1, FA_DTYPE_FP32 = 2 /* fa_combine output only */ } fa_dtype_t;
+
+typedef enum {
+    FA_KIND_KVCACHE = 0,  /* flash_attn_with_kvcache */
+    FA_KIND_DENSE = 1,    /* flash_attn_func */
+    FA_KIND_VARLEN = 2    /* flash_attn_varlen_func */
+} fa_kind_t;
+
+typedef struct fa_fwd_params {
+    int32_t abi_version;  /* FA_MI355X_ABI_VERSION */
+    int32_t dtype;        /* fa_dtype_t, shared by q, k, v, k_new, v_new, out, rotary cos/sin */
+
+    int32_t batch;        /* B (query batch) */
+    int32_t seqlen_q;     /* Sq (dense/kvcache), max_seqlen_q (varlen) */
+    int32_t nheads;       /* H */
+    int32_t nheads_k;     /* Hk, H % Hk == 0 */
+    int32_t headdim;      /* D */
+    int32_t headdim_v;    /* Dv (must equal D) */
+    int32_t seqlen_k;     /* dense: Sk; kvcache contiguous: seqlen_cache; varlen: max_seqlen_k */
+    int32_t batch_cache;  /* kvcache contiguous: rows of k/v cache; paged: num_blocks */
+    int32_t total_q;      /* varlen: rows of q */
+
+    /* q: (B, Sq, H, D) or varlen (total_q, H, D) */
+    const void* q;
+    int64_t q_batch_stride, q_row_stride, q_head_stride;
+    /* k/v: dense (B, Sk, Hk, D); kvcache (Bc, Sc, Hk, D) or paged (num_blocks, page, Hk, D);
+       varlen (total_k, Hk, D). Mutated in place when k_new/v_new are given. */
+    void* k;
+    int64_t k_batch_stride, k_row_stride, k_head_stride;
+    void* v;
+    int64_t v_batch_stride, v_row_stride, v_head_stride;
+    /* kvcache only: new tokens (B, seqlen_new, Hk, D) appended at cache_seqlens */
+    const void* k_new;
+    int64_t knew_batch_stride, knew_row_stride, knew_head_stride;
+    const void* v_new;
+    int64_t vnew_batch_stride, vnew_row_stride, vnew_head_stride;
+    int32_t seqlen_new;
+
+    /* out: like q; softmax_lse: (B, H, Sq) fp32, varlen (H, total_q) fp32 */
+    void* out;
+    int64_t out_batch_stride, out_row_stride, out_head_stride;
+    float* softmax_lse;
+
+    const int32_t* cache_seqlens;   /* kvcache: (B,) int32, tokens already cached */
+    const int32_t* cu_seqlens_q;    /* varlen: (B+1,) */
+    const int32_t* cu_seqlens_k;    /* varlen: (B+1,) */
+    const int32_t* block_table;     /* paged: (B or Bc, max_blocks) int32 */
+    int64_t block_table_batch_stride;
+    int32_t max_blocks_per_seq;
+    int32_t block_table_rows;       /* rows of block_table (cache_batch_idx values index them) */
+    int32_t page_block_size;
+    const int32_t* cache_batch_idx; /* kvcache: (B,) rows of the cache / block table */
+
+    const void* rotary_cos;         /* (seqlen_ro, rotary_dim/2), dtype as q */
+    const void* rotary_sin;
+    int32_t rotary_dim;
+    int32_t seqlen_ro;
+    int32_t rotary_interleaved;
+
+    const float* alibi_slopes;      /* (H,) or (B, H) fp32 */
+    int64_t alibi_batch_stride;     /* 0 for (H,), H for (B, H) */
+
+    float softmax_scale;
+    float softcap;                  /* 0 = off */
+    float dropout_p;                /* must be 0 (forward inference only) */
+    int32_t is_causal;
+    int32_t window_size_left;       /* -1 = unbounded */
+    int32_t window_size_right;
+    int32_t num_splits;             /* 0 = heuristic, 1 = no split, n > 1 = n chunks */
+
+    void* workspace;
+    size_t workspace_bytes;
+} fa_fwd_params;
+
+/* Library / ABI version. */
+int fa_abi_version(void);
+
+/* Host-only validation of `p` for the given kind; never touches the GPU. */
+fa_status_t fa_validate(const fa_fwd_params* p, int32_t kind);
+
+/* Bytes of workspace the call needs (host-only; 0 is possible). */
+fa_status_t fa_fwd_workspace_size(const fa_fwd_params* p, int32_t kind, size_t* bytes);
+
+/* Forward passes; enqueue on `stream` (hipStream_t). */
+fa_status_t fa_mha_fwd_kvcache(const fa_fwd_params* p, void* stream);
+fa_status_t fa_mha_fwd(const fa_fwd_params* p, void* stream);
+fa_status_t fa_mha_varlen_fwd(const fa_fwd_params* p, void* stream);
+
+/* Split-KV merge: out_partial (S, R, Dv) fp32, lse_partial (S, R) fp32 ->
+ * out (R, Dv) in `out_dtype` (row stride out_row_stride elements),
+ * lse (R,) fp32. Rows with no finite partial LSE get out = 0, lse = +inf. */
+fa_status_t fa_combine(const float* out_partial, const float* lse_partial, int32_t num_splits, int64_t rows,
+                       int32_t headdim_v, void* out, int64_t out_row_stride, int32_t out_dtype, float* lse,
+                       void* stream);
+
+/* Thread-local message describing the last non-FA_OK status on this thread. */
+const char* fa_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FA_MI355X_H */
