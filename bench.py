@@ -1,0 +1,377 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X FlashAttention forward path on the BASELINE configs.
+
+One JSON line on stdout. The headline (`value`) is BASELINE config 2 -- the
+contiguous-KV GQA decode with a 1-token in-place append (B=32, H=32/8, D=128,
+bf16, caches (32, 8192, 8, 128), cache_seqlens ~ U[1024, 8191]) -- as
+algorithmic HBM TB/s of the whole call (append + attention + combine), inputs
+resident in HBM. Configs 3-5 are reported in `configs` beside it; config 1 is
+the CPU-runnable parity anchor and is not a bench line.
+
+Every call goes through the C ABI (libfa_mi355x.so via ctypes); PyTorch only
+allocates device memory and supplies the stream. Kernel durations come from
+HIP events recorded by the library at stage boundaries (fa_fwd_params.
+stage_events) on the stream the kernels run on. Caches are rotated between
+copies so reads are not served by the 256 MB Infinity Cache.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c3,c4,c5] [--no-cpu]
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (REPO, os.path.join(REPO, "flash-attention-npu_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+METRIC = "decode attn µs/call + achieved HBM TB/s; prefill TFLOP/s (% bf16 MFMA peak)"
+
+
+# ---- HIP events through the runtime's C API --------------------------------------------------
+class Hip:
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+
+    def event(self):
+        e = ctypes.c_void_p()
+        assert self.lib.hipEventCreate(ctypes.byref(e)) == 0
+        return e
+
+    def record(self, e, stream):
+        assert self.lib.hipEventRecord(e, stream) == 0
+
+    def ms(self, a, b):
+        assert self.lib.hipEventSynchronize(b) == 0
+        out = ctypes.c_float()
+        assert self.lib.hipEventElapsedTime(ctypes.byref(out), a, b) == 0
+        return out.value
+
+
+# ---- config builders --------------------------------------------------------------------------
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def build_case(name, torch, dev, ncopy):
+    """Returns dict with per-copy C-ABI params, algorithmic work, host slices for the CPU baseline."""
+    from fa_mi355x import capi
+    g = torch.Generator(device=dev)
+    gc = torch.Generator()
+    bf = torch.bfloat16
+    D = 128
+    keep = []
+
+    def rn(*shape):
+        t = torch.randn(shape, generator=g, device=dev, dtype=torch.float32).to(bf)
+        return t
+
+    c = {"name": name}
+    if name == "c2":
+        g.manual_seed(2); gc.manual_seed(2)
+        B, Sq, H, Hk, cap = 32, 1, 32, 8, 8192
+        L = torch.randint(1024, 8192, (B,), generator=gc, dtype=torch.int32)
+        q, kn, vn = rn(B, Sq, H, D), rn(B, 1, Hk, D), rn(B, 1, Hk, D)
+        caches = [(rn(B, cap, Hk, D), rn(B, cap, Hk, D)) for _ in range(ncopy)]
+        bt = None
+        bidx = None
+        window, alibi, cos, sin = (-1, -1), None, None, None
+        s_new = 1
+        kv_tokens = int((L + 1).sum())
+        c["work_desc"] = "B32 Sq1 H32/8 D128 bf16 contiguous cache 32x8192, L~U[1024,8191], 1-token append"
+    elif name == "c3":
+        g.manual_seed(3); gc.manual_seed(3)
+        B, Sq, H, Hk, page = 64, 1, 64, 8, 256
+        L = torch.round(torch.exp(torch.empty(B).uniform_(math.log(512), math.log(32768), generator=gc))).to(torch.int32)
+        need = ((L + 1 + page - 1) // page).tolist()
+        nblocks = int(sum(int(math.ceil(int(x) / page)) for x in L) * 1.1) + 1
+        nblocks = max(nblocks, sum(need))
+        perm = torch.randperm(nblocks, generator=gc).to(torch.int32)
+        maxb = max(need)
+        bt_h = torch.zeros((B, maxb), dtype=torch.int32)
+        o = 0
+        for b in range(B):
+            bt_h[b, :need[b]] = perm[o:o + need[b]]
+            o += need[b]
+        bt = bt_h.to(dev)
+        q, kn, vn = rn(B, Sq, H, D), rn(B, 1, Hk, D), rn(B, 1, Hk, D)
+        caches = [(rn(nblocks, page, Hk, D), rn(nblocks, page, Hk, D)) for _ in range(ncopy)]
+        bidx = None
+        window, alibi, cos, sin = (-1, -1), None, None, None
+        s_new = 1
+        kv_tokens = int((L + 1).sum())
+        cap = maxb * page
+        c["work_desc"] = "B64 Sq1 H64/8 D128 bf16 paged(256) permuted block_table, L log-uniform [512,32768], 1-token append"
+    elif name == "c4":
+        g.manual_seed(4); gc.manual_seed(4)
+        B, Sq, H, Hk, cap = 4, 2048, 32, 8, 8192
+        L = torch.full((B,), 6144, dtype=torch.int32)
+        q, kn, vn = rn(B, Sq, H, D), rn(B, Sq, Hk, D), rn(B, Sq, Hk, D)
+        caches = [(rn(B, cap, Hk, D), rn(B, cap, Hk, D)) for _ in range(ncopy)]
+        inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+        ang = torch.arange(cap, dtype=torch.float32)[:, None] * inv[None, :]
+        cos, sin = torch.cos(ang).to(bf).to(dev), torch.sin(ang).to(bf).to(dev)
+        bt = None
+        bidx = None
+        window, alibi = (-1, -1), None
+        s_new = Sq
+        kv_tokens = None
+        c["work_desc"] = "B4 2048 new tokens onto 6144 cached (cache 8192), H32/8 D128 bf16, NeoX rotary, causal"
+    elif name == "c5":
+        g.manual_seed(5); gc.manual_seed(5)
+        B, Sq, H, Hk, page = 8, 4, 32, 8, 256
+        L = torch.randint(16384, 65537, (B,), generator=gc, dtype=torch.int32)
+        bidx_h = torch.randperm(B, generator=gc).to(torch.int32)
+        need_rows = [0] * B
+        for b in range(B):
+            need_rows[int(bidx_h[b])] = (int(L[b]) + page - 1) // page
+        nblocks = int(sum(need_rows) * 1.1) + 1
+        perm = torch.randperm(nblocks, generator=gc).to(torch.int32)
+        maxb = max(need_rows)
+        bt_h = torch.zeros((B, maxb), dtype=torch.int32)
+        o = 0
+        for r in range(B):
+            bt_h[r, :need_rows[r]] = perm[o:o + need_rows[r]]
+            o += need_rows[r]
+        bt = bt_h.to(dev)
+        bidx = bidx_h.to(dev)
+        q = rn(B, Sq, H, D)
+        kn = vn = None
+        caches = [(rn(nblocks, page, Hk, D), rn(nblocks, page, Hk, D)) for _ in range(ncopy)]
+        window = (4096, 0)
+        alibi = torch.tensor([2.0 ** (-8.0 * (h + 1) / H) for h in range(H)], dtype=torch.float32, device=dev)
+        cos = sin = None
+        s_new = 0
+        kv_tokens = None
+        cap = maxb * page
+        c["work_desc"] = "B8 Sq4 H32/8 D128 bf16 paged(256), L~U[16384,65536], cache_batch_idx perm, window (4096,0), ALiBi"
+    else:
+        raise ValueError(name)
+
+    sl = L.to(dev)
+    out = torch.empty((B, Sq, H, D), dtype=bf, device=dev)
+    lse = torch.empty((B, H, Sq), dtype=torch.float32, device=dev)
+    params = []
+    for (kc, vc) in caches:
+        p = capi.new_params(
+            dtype=capi.FA_DTYPE_BF16, batch=B, seqlen_q=Sq, nheads=H, nheads_k=Hk, headdim=D, headdim_v=D,
+            seqlen_k=kc.shape[1] if bt is None else 0, batch_cache=kc.shape[0],
+            q=_ptr(q), q_batch_stride=q.stride(0), q_row_stride=q.stride(1), q_head_stride=q.stride(2),
+            k=_ptr(kc), k_batch_stride=kc.stride(0), k_row_stride=kc.stride(1), k_head_stride=kc.stride(2),
+            v=_ptr(vc), v_batch_stride=vc.stride(0), v_row_stride=vc.stride(1), v_head_stride=vc.stride(2),
+            out=_ptr(out), out_batch_stride=out.stride(0), out_row_stride=out.stride(1),
+            out_head_stride=out.stride(2), softmax_lse=_ptr(lse), cache_seqlens=_ptr(sl),
+            softmax_scale=D ** -0.5, is_causal=1, window_size_left=window[0], window_size_right=window[1])
+        if kn is not None:
+            p.k_new, p.v_new = _ptr(kn), _ptr(vn)
+            p.knew_batch_stride, p.knew_row_stride, p.knew_head_stride = kn.stride(0), kn.stride(1), kn.stride(2)
+            p.vnew_batch_stride, p.vnew_row_stride, p.vnew_head_stride = vn.stride(0), vn.stride(1), vn.stride(2)
+            p.seqlen_new = s_new
+        if bt is not None:
+            p.block_table = _ptr(bt)
+            p.block_table_batch_stride = bt.stride(0)
+            p.max_blocks_per_seq = bt.shape[1]
+            p.block_table_rows = bt.shape[0]
+            p.page_block_size = kc.shape[1]
+        if bidx is not None:
+            p.cache_batch_idx = _ptr(bidx)
+        if cos is not None:
+            p.rotary_cos, p.rotary_sin = _ptr(cos), _ptr(sin)
+            p.rotary_dim, p.seqlen_ro, p.rotary_interleaved = 2 * cos.shape[1], cos.shape[0], 0
+        if alibi is not None:
+            p.alibi_slopes = _ptr(alibi)
+        st, nbytes = capi.workspace_size(p, capi.FA_KIND_KVCACHE)
+        assert st == 0, capi.last_error()
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+        keep.append(ws)
+        p.workspace, p.workspace_bytes = _ptr(ws), ws.numel()
+        params.append(p)
+
+    # algorithmic work (per call)
+    e = 2
+    if name in ("c2", "c3"):
+        kv = 2 * kv_tokens * Hk * D * e                      # K and V of L+1 tokens
+        qo = 2 * B * Sq * H * D * e + 4 * B * H * Sq          # q read, out write, lse write
+        app = 2 * 2 * B * Hk * D * e                          # new k/v read + cache write
+        c["attn_bytes"] = kv + qo
+        c["bytes"] = kv + qo + app
+        c["bound"] = "hbm"
+    elif name == "c5":
+        keys = 0
+        for b in range(B):
+            Lb = int(L[b])
+            lo = max(0, Lb - Sq - 4096)     # union of the 4 rows' windows
+            keys += Lb - lo
+        c["attn_bytes"] = 2 * keys * Hk * D * e + 2 * B * Sq * H * D * e + 4 * B * H * Sq
+        c["bytes"] = c["attn_bytes"]
+        c["bound"] = "hbm"
+    else:  # c4
+        P = sum(6145 + i for i in range(2048))
+        c["flops"] = 4 * D * P * B * H
+        c["bound"] = "mfma"
+    c.update(params=params, keep=[q, kn, vn, caches, bt, bidx, cos, sin, alibi, out, lse, sl],
+             B=B, Sq=Sq, H=H, Hk=Hk, L=L)
+    return c
+
+
+def time_case(c, hip, torch, steps, warmup):
+    from fa_mi355x import capi
+    L = capi.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    ps = c["params"]
+    n = len(ps)
+
+    def call(i, ev=None):
+        p = ps[i % n]
+        p.stage_events = ev
+        st = L.fa_mha_fwd_kvcache(ctypes.byref(p), stream)
+        if st != 0:
+            raise RuntimeError(capi.last_error())
+
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize()
+    # pass 1: whole calls, back to back
+    a, b = hip.event(), hip.event()
+    hip.record(a, stream)
+    for i in range(steps):
+        call(i)
+    hip.record(b, stream)
+    whole_ms = hip.ms(a, b) / steps
+    torch.cuda.synchronize()
+    # pass 2: per-stage events (append | attention | combine)
+    evs = [[hip.event() for _ in range(4)] for _ in range(steps)]
+    arrs = [(ctypes.c_void_p * 4)(*[e.value for e in ev]) for ev in evs]
+    for i in range(steps):
+        call(i, ctypes.cast(arrs[i], ctypes.c_void_p))
+    torch.cuda.synchronize()
+    st = [[hip.ms(ev[k], ev[k + 1]) for k in range(3)] for ev in evs]
+    mean = lambda xs: sum(xs) / len(xs)
+    return {"us_per_call": whole_ms * 1e3,
+            "append_us": mean([s[0] for s in st]) * 1e3,
+            "attn_us": mean([s[1] for s in st]) * 1e3,
+            "combine_us": mean([s[2] for s in st]) * 1e3}
+
+
+def cpu_baseline(c, torch):
+    """The oracle (C restatement of the reference golden) on the host cores, on
+    a bounded sample of config 2: the first `nb` sequences, all heads."""
+    import numpy as np
+    from oracle import fa_oracle as orc
+    nthreads = min(16, os.cpu_count() or 1)
+    B = c["B"]
+    q, kn, vn, caches = c["keep"][0], c["keep"][1], c["keep"][2], c["keep"][3]
+    kc, vc = caches[0]
+    L = c["L"]
+    nb = min(B, 8)
+    bits = lambda t: t[:nb].contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+    qh, kh, vh, knh, vnh = bits(q), bits(kc), bits(vc), bits(kn), bits(vn)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        orc.kvcache_forward(qh, kh, vh, dtype=orc.BF16, cache_seqlens=L[:nb].numpy(), k=knh, v=vnh, causal=True,
+                            nthreads=nthreads)
+        reps += 1
+        if time.perf_counter() - t0 > 10.0 or reps >= 20:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    Hk, D = c["Hk"], 128
+    Ls = L[:nb]
+    sample_bytes = 2 * int((Ls + 1).sum()) * Hk * D * 2 + 2 * nb * c["H"] * D * 2 + 4 * nb * c["H"] + 2 * 2 * nb * Hk * D * 2
+    return {"value": sample_bytes / dt / 1e12, "unit": "TB/s", "cores": nthreads, "kind": "port",
+            "sample": f"config 2, sequences 0..{nb - 1} of {B} (all 32 q heads), oracle/fa_oracle.c with "
+                      f"{nthreads} OpenMP threads, {reps} reps, {dt * 1e3:.1f} ms/rep"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--configs", default="c2,c3,c4,c5")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "the per-GPU shard of the decode/prefill work is the single-GPU workload reported with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import fa_mi355x  # noqa: F401  (fails loudly without the built HIP library)
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = "cuda"
+    hip = Hip()
+    names = [s.strip() for s in args.configs.split(",") if s.strip()]
+    if "c2" not in names:
+        names = ["c2"] + names
+    results = {}
+    cases = {}
+    for name in names:
+        ncopy = {"c2": 2, "c3": 2, "c4": 1, "c5": 4}[name]
+        c = build_case(name, torch, dev, ncopy)
+        torch.cuda.synchronize()
+        t = time_case(c, hip, torch, args.steps, args.warmup)
+        r = dict(t)
+        r["workload"] = c["work_desc"]
+        if c["bound"] == "hbm":
+            r["bytes_per_call"] = c["bytes"]
+            r["tbps_call"] = c["bytes"] / (t["us_per_call"] * 1e-6) / 1e12
+            r["attn_bytes"] = c["attn_bytes"]
+            r["attn_tbps"] = c["attn_bytes"] / (t["attn_us"] * 1e-6) / 1e12
+            r["attn_frac_hbm"] = r["attn_tbps"] * 1e3 / HBM_PEAK_GBS
+        else:
+            r["flops_per_call"] = c["flops"]
+            r["tflops_call"] = c["flops"] / (t["us_per_call"] * 1e-6) / 1e12
+            r["attn_tflops"] = c["flops"] / (t["attn_us"] * 1e-6) / 1e12
+            r["attn_frac_mfma"] = r["attn_tflops"] / BF16_PEAK_TFLOPS
+        results[name] = r
+        print(f"# {name}: {json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})}",
+              file=sys.stderr, flush=True)
+        if name == "c2":
+            cases["c2"] = c
+        else:
+            del c
+            torch.cuda.empty_cache()
+
+    c2 = results["c2"]
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cases["c2"], torch)
+    line = {
+        "metric": METRIC,
+        "value": round(c2["tbps_call"], 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c2["us_per_call"] / 1e3, 6),
+        "us_per_call": round(c2["us_per_call"], 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1))",
+        "config": {"workload": "BASELINE config 2: " + c2["workload"], "batch": 32, "nheads": 32, "nheads_k": 8,
+                   "headdim": 128, "seqlen_cache": 8192, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(c2["attn_tbps"] * 1e3, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(c2["attn_frac_hbm"], 4), "traffic": None,
+                     "kernel": "fa_fwd_kernel (decode config)", "kernel_us": round(c2["attn_us"], 2)},
+        "cpu_baseline": cpu,
+        "configs": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in results.items()},
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -23,7 +23,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = os.environ.get("FA_MI355X_ARCH", "gfx950")
 
-HIP_SOURCES = ["fa_fwd.hip", "fa_kv_prep.hip", "fa_api.cpp"]
+HIP_SOURCES = ["fa_fwd.hip", "fa_decode.hip", "fa_kv_prep.hip", "fa_api.cpp"]
 HIPFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     # no packed fp32 ops (v_pk_*_f32) in any generated code
@@ -78,7 +78,7 @@ def build(jobs=8, verbose=True):
         tfut.result()
     core = os.path.join(LIBDIR, "libfa_mi355x.so")
     tmp = core + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs)
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", tmp] + objs)
     os.replace(tmp, core)
     tlib = os.path.join(LIBDIR, "libfa_mi355x_torch.so")
     tmp = tlib + ".tmp"

@@ -14,6 +14,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 
@@ -21,10 +22,12 @@
 #include "fa_kernel_args.h"
 
 namespace fa {
-int fwd_tile_rows(bool decode);
-int fwd_tile_keys(bool decode);
-hipError_t launch_fwd(const FwdArgs& a, int dtype, int d, bool decode, int grid, hipStream_t stream);
-hipError_t launch_combine(const CombineArgs& c, int dtype, int d, int grid, hipStream_t stream);
+int fwd_tile_rows();
+int fwd_tile_keys();
+int decode_workers(int cus);
+hipError_t launch_fwd(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream);
+hipError_t launch_merge(const FwdArgs& a, int dtype, int d, hipStream_t stream);
+hipError_t launch_decode(const FwdArgs& a, int dtype, int grid, hipStream_t stream);
 hipError_t launch_combine_flat(const float* po, const float* pl, int S, int64_t R, int Dv, void* out, int64_t ors,
                                int out_dtype, float* lse, hipStream_t stream);
 hipError_t launch_kv_prep(const KvPrepArgs& a, int dtype, hipStream_t stream);
@@ -82,6 +85,7 @@ struct Plan {
     int64_t items_max;  // bound on work items (partial buffer size)
     int grid;
     bool rotary;
+    int workers;        // decode: wave workers
     size_t off_sched, off_plse, off_po, off_qrot, total;
 };
 
@@ -136,6 +140,9 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
             FA_CHECK(p->seqlen_new >= 1, "k/v must have at least one new token");
             FA_CHECK(p->cache_seqlens != nullptr, "cache_seqlens is required to append k/v");
             FA_CHECK(aligned16(p->k_new) && aligned16(p->v_new), "k and v must be 16-byte aligned");
+            FA_CHECK(strides8(p->knew_batch_stride, p->knew_row_stride, p->knew_head_stride) &&
+                         strides8(p->vnew_batch_stride, p->vnew_row_stride, p->vnew_head_stride),
+                     "k and v strides must be multiples of 8 elements");
         }
         if (p->rotary_cos || p->rotary_sin) {
             FA_CHECK(p->rotary_cos && p->rotary_sin, "rotary_cos and rotary_sin must be given together");
@@ -143,6 +150,9 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
             FA_CHECK(p->rotary_dim > 0 && p->rotary_dim % 16 == 0, "rotary_dim must be divisible by 16");
             FA_CHECK(p->rotary_dim <= p->headdim, "rotary_dim must be <= headdim");
             FA_CHECK(p->seqlen_ro >= 1, "rotary_cos must have at least one row");
+            FA_CHECK((reinterpret_cast<uintptr_t>(p->rotary_cos) & 7u) == 0 &&
+                         (reinterpret_cast<uintptr_t>(p->rotary_sin) & 7u) == 0,
+                     "rotary_cos/sin must be 8-byte aligned");
         }
     } else {
         FA_CHECK(p->k_new == nullptr && p->v_new == nullptr, "k_new/v_new are only valid for the kvcache forward");
@@ -167,8 +177,8 @@ void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
     pl.g = p->nheads / p->nheads_k;
     pl.rows_max = p->seqlen_q * pl.g;
     pl.decode = pl.rows_max <= kDecodeRows;
-    pl.BM = fa::fwd_tile_rows(pl.decode);
-    pl.BN = fa::fwd_tile_keys(pl.decode);
+    pl.BM = pl.decode ? kDecodeRows : fa::fwd_tile_rows();
+    pl.BN = pl.decode ? 32 : fa::fwd_tile_keys();
     pl.mt_max = (pl.rows_max + pl.BM - 1) / pl.BM;
     if (pl.mt_max < 1) pl.mt_max = 1;
     if (kind == FA_KIND_KVCACHE) {
@@ -181,29 +191,34 @@ void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
         pl.kv_capacity = p->seqlen_k;
     }
     const int cus = cu_count();
-    const int occ = 2;  // workgroups per CU for both kernel shapes
-    const int64_t base_bound = (int64_t)p->batch * p->nheads_k * pl.mt_max;
-    pl.target_items = (pl.decode ? 8 : 4) * cus;
-    pl.min_chunk = 2 * pl.BN;
-    if (p->num_splits == 1) {
-        pl.allow_split = false;
-    } else if (p->num_splits > 1) {
-        pl.allow_split = true;
-    } else {
-        pl.allow_split = pl.decode || base_bound < cus;
-    }
-    if (!pl.allow_split) pl.items_max = base_bound;
-    else if (p->num_splits > 1) pl.items_max = base_bound * p->num_splits;
-    else pl.items_max = base_bound + pl.target_items;
-    const int64_t persistent = (int64_t)occ * cus;
-    if (pl.allow_split || pl.decode) pl.grid = (int)std::min<int64_t>(pl.items_max, persistent);
-    else pl.grid = (int)std::min<int64_t>(pl.items_max, INT_MAX);
-    if (pl.grid < 1) pl.grid = 1;
     pl.rotary = kind == FA_KIND_KVCACHE && p->rotary_cos != nullptr;
-
     size_t off = 0;
     pl.off_sched = off;
     off = align256(off + sizeof(int) * (2 * (size_t)p->batch + 2));
+    if (pl.decode) {
+        // stream-K decode: one workgroup of 4 wave workers per CU, <= 2 partials per worker
+        pl.grid = cus;
+        pl.workers = fa::decode_workers(cus);
+        pl.allow_split = true;
+        pl.items_max = (int64_t)pl.workers * 2;
+        pl.target_items = 0;
+        pl.min_chunk = 0;
+    } else {
+        const int occ = 2;  // prefill workgroups per CU
+        const int64_t base_bound = (int64_t)p->batch * p->nheads_k * pl.mt_max;
+        pl.workers = 0;
+        pl.target_items = 4 * cus;
+        pl.min_chunk = 2 * pl.BN;
+        if (p->num_splits == 1) pl.allow_split = false;
+        else if (p->num_splits > 1) pl.allow_split = true;
+        else pl.allow_split = base_bound < cus;
+        if (!pl.allow_split) pl.items_max = base_bound;
+        else if (p->num_splits > 1) pl.items_max = base_bound * p->num_splits;
+        else pl.items_max = base_bound + pl.target_items;
+        if (pl.allow_split) pl.grid = (int)std::min<int64_t>(pl.items_max, (int64_t)occ * cus);
+        else pl.grid = (int)std::min<int64_t>(pl.items_max, INT_MAX);
+        if (pl.grid < 1) pl.grid = 1;
+    }
     pl.off_plse = off;
     if (pl.allow_split) off = align256(off + sizeof(float) * (size_t)pl.items_max * pl.BM);
     pl.off_po = off;
@@ -233,6 +248,10 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
     const void* q_ptr = p->q;
     int64_t q_sb = p->q_batch_stride, q_si = p->q_row_stride, q_sh = p->q_head_stride;
 
+    auto mark = [&](int i) {
+        if (p->stage_events && p->stage_events[i]) (void)hipEventRecord(static_cast<hipEvent_t>(p->stage_events[i]), stream);
+    };
+    mark(0);
     if (kind == FA_KIND_KVCACHE && p->k_new) {
         fa::KvPrepArgs k{};
         k.k_new = p->k_new;
@@ -352,33 +371,24 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
     a.num_splits = p->num_splits > 1 ? p->num_splits : 0;
     a.target_items = pl.target_items;
     a.min_chunk = pl.min_chunk;
-
-    hipError_t e = fa::launch_fwd(a, p->dtype, p->headdim, pl.decode, pl.grid, stream);
-    if (e != hipSuccess) return fail(FA_EHIP, "attention launch failed: %s", hipGetErrorString(e));
-    if (pl.allow_split) {
-        fa::CombineArgs c{};
-        c.out = p->out;
-        c.o_sb = a.o_sb;
-        c.o_si = a.o_si;
-        c.o_sh = a.o_sh;
-        c.lse = a.lse;
-        c.lse_sb = a.lse_sb;
-        c.lse_sh = a.lse_sh;
-        c.part_o = a.part_o;
-        c.part_lse = a.part_lse;
-        c.sched = a.sched;
-        c.cu_seqlens_q = a.cu_seqlens_q;
-        c.B = p->batch;
-        c.Sq = p->seqlen_q;
-        c.H = p->nheads;
-        c.Hk = p->nheads_k;
-        c.g = pl.g;
-        c.BM = pl.BM;
-        c.mt_max = pl.mt_max;
-        int grid = (int)std::min<int64_t>((int64_t)p->batch * p->nheads_k * pl.mt_max, INT_MAX);
-        e = fa::launch_combine(c, p->dtype, p->headdim, grid, stream);
-        if (e != hipSuccess) return fail(FA_EHIP, "combine launch failed: %s", hipGetErrorString(e));
+    a.mt_max = pl.mt_max;
+    a.page_shift = -1;
+    if (paged && (p->page_block_size & (p->page_block_size - 1)) == 0) {
+        int sh = 0;
+        while ((1 << sh) < p->page_block_size) ++sh;
+        a.page_shift = sh;
     }
+
+    mark(1);
+    hipError_t e = pl.decode ? fa::launch_decode(a, p->dtype, pl.grid, stream)
+                             : fa::launch_fwd(a, p->dtype, p->headdim, pl.grid, stream);
+    if (e != hipSuccess) return fail(FA_EHIP, "attention launch failed: %s", hipGetErrorString(e));
+    mark(2);
+    if (!pl.decode && pl.allow_split) {
+        hipError_t em = fa::launch_merge(a, p->dtype, p->headdim, stream);
+        if (em != hipSuccess) return fail(FA_EHIP, "merge launch failed: %s", hipGetErrorString(em));
+    }
+    mark(3);
     return FA_OK;
 }
 

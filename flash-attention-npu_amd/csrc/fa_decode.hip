@@ -1,0 +1,482 @@
+// fa_decode.hip -- decode attention for gfx950 (<= 16 packed query rows per kv
+// head): KV-cache streaming at HBM speed.
+//
+// Same results as the reference forward (SplitFuse::FAInfer in flash-decode
+// mode, csrc/arch22/flash_attn_npu_v2/mha_fwd_kvcache.cpp:250-316 with the
+// CombineScale merge at :412-433 and CombineScale.hpp:76-357), organised for
+// MI355X instead of the reference's per-core (B, N1, S1, S2) ranges
+// (csrc/arch22/flash_attn_npu_v3/fa_split.h:483-510):
+//   * The work list is every 32-key tile of every (sequence, kv head)
+//     "segment", built in LDS from cache_seqlens by each workgroup (no host
+//     round trip). The tiles are cut into equal contiguous ranges, one per
+//     wave ("worker"), so uneven sequence lengths still balance exactly.
+//   * A worker streams its tiles with a STAGES-deep register pipeline of
+//     16-byte loads (K straight into MFMA operand layout, V through a
+//     wave-private LDS tile read back transposed), so each wave keeps up to
+//     (STAGES-1) x 16 KB of HBM reads in flight without any block barrier.
+//   * The g = H/Hk query heads of a kv head (x the query positions) form the
+//     16 rows of one MFMA tile, so every cache byte is read once per call.
+//   * A segment owned entirely by one worker is written final; a segment cut
+//     by worker boundaries leaves <= 2 fp32 partials per worker, merged by
+//     fa_decode_merge_kernel (the kernel boundary orders the partials).
+#include "fa_common.h"
+#include "fa_kernel_args.h"
+
+namespace fa {
+namespace dec {
+constexpr int D = 128;
+constexpr int KT = 32;       // keys per tile
+constexpr int NWAVE = 4;     // waves (workers) per workgroup
+constexpr int KSTEPS = D / 32;
+constexpr int DBLK = D / 16;
+constexpr int SWZ = 15;
+constexpr int TABN = 256;    // paged: block ids staged per wave
+constexpr int MAXB = 2048;
+}  // namespace dec
+
+struct DecSeg {
+    int S, n;         // first global tile, tiles
+    int b, hk;
+    int lo_tile;      // first 32-key tile of the sequence's visible key range
+    int sk, sq, crow;
+};
+
+// Per-batch facts kept in LDS: first tile, key count, query count, cache row.
+struct DecBatch {
+    int lo_tile, sk, sq, crow;
+};
+
+__device__ __forceinline__ void dec_batch(const FwdArgs& a, int b, DecBatch& d, int& ntiles) {
+    int sq = a.cu_seqlens_q ? a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b] : a.Sq;
+    int sk;
+    if (a.seqlens_k) sk = a.seqlens_k[b] + a.seqlen_new;
+    else if (a.cu_seqlens_k) sk = a.cu_seqlens_k[b + 1] - a.cu_seqlens_k[b];
+    else sk = a.Sk;
+    sq = min(max(sq, 0), a.Sq);
+    sk = min(max(sk, 0), a.kv_capacity);
+    int lo = a.wl >= 0 ? max(0, sk - sq - a.wl) : 0;
+    int hi = a.wr >= 0 ? min(sk, sk - 1 + a.wr + 1) : sk;
+    d.sq = sq;
+    d.sk = sk;
+    d.lo_tile = lo / dec::KT;
+    const int bt_rows_or_cache = a.block_table ? a.bt_rows : a.batch_cache;
+    d.crow = a.batch_idx ? min(max(a.batch_idx[b], 0), bt_rows_or_cache - 1) : b;
+    ntiles = (sq > 0 && hi > lo) ? (hi + dec::KT - 1) / dec::KT - d.lo_tile : 0;
+}
+
+__device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref, const DecBatch* s_b, int t) {
+    int bl = 0, bh = a.B;
+    while (bh - bl > 1) {
+        int mid = (bl + bh) >> 1;
+        if (s_pref[mid] <= t) bl = mid; else bh = mid;
+    }
+    DecSeg s;
+    s.b = bl;
+    const int per = (s_pref[bl + 1] - s_pref[bl]) / a.Hk;
+    s.n = per;
+    const int o = t - s_pref[bl];
+    s.hk = per > 0 ? o / per : 0;
+    s.S = s_pref[bl] + s.hk * per;
+    const DecBatch d = s_b[bl];
+    s.lo_tile = d.lo_tile;
+    s.sk = d.sk;
+    s.sq = d.sq;
+    s.crow = d.crow;
+    return s;
+}
+
+template <int DT, int STAGES>
+__global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
+    using namespace dec;
+    __shared__ int s_pref[MAXB + 1];
+    __shared__ DecBatch s_bat[MAXB];
+    __shared__ int s_tab[NWAVE][TABN];
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[NWAVE][KT * D];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, G = lane >> 4;
+
+    // ---- plan: tiles per segment, prefix over batches -------------------------------
+    for (int b = tid; b < a.B; b += 256) {
+        DecBatch d;
+        int nt;
+        dec_batch(a, b, d, nt);
+        s_bat[b] = d;
+        s_pref[b + 1] = a.Hk * nt;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const int seg = (a.B + 63) / 64, b0 = lane * seg;
+        int local = 0;
+        for (int k = 0; k < seg; ++k)
+            if (b0 + k < a.B) local += s_pref[b0 + k + 1];
+        int incl = local;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            int v = __shfl_up(incl, o);
+            if (lane >= o) incl += v;
+        }
+        int run = incl - local;
+        for (int k = 0; k < seg; ++k)
+            if (b0 + k < a.B) {
+                run += s_pref[b0 + k + 1];
+                s_pref[b0 + k + 1] = run;
+            }
+        if (lane == 0) s_pref[0] = 0;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0)
+        for (int b = tid; b <= a.B; b += 256) a.sched[b] = s_pref[b];
+
+    const long long T = s_pref[a.B];
+    const long long W = (long long)gridDim.x * NWAVE;
+    const long long wid = (long long)blockIdx.x * NWAVE + wave;
+    const int t0 = (int)(wid * T / W), t1 = (int)((wid + 1) * T / W);
+    if (t0 >= t1) return;  // no block barrier follows: waves are independent from here
+
+    const uint16_t* qp = static_cast<const uint16_t*>(a.q);
+    const uint16_t* kp = static_cast<const uint16_t*>(a.k);
+    const uint16_t* vp = static_cast<const uint16_t*>(a.v);
+    uint16_t* sv = s_v[wave];
+    int* tab = s_tab[wave];
+    const bool paged = a.block_table != nullptr;
+    const bool tab_ok = paged && (a.page % KT) == 0;
+    int tab_base = t0;
+
+    auto fill_tab = [&](int base) {
+        for (int i = lane; i < TABN; i += 64) {
+            const int t = base + i;
+            int blk = 0;
+            if (t < t1) {
+                DecSeg s = dec_seg_of(a, s_pref, s_bat, t);
+                const int key0 = (s.lo_tile + (t - s.S)) * KT;
+                const int pidx = a.page_shift >= 0 ? key0 >> a.page_shift : key0 / a.page;
+                blk = a.block_table[(int64_t)s.crow * a.bt_stride + pidx];
+                blk = min(max(blk, 0), a.num_blocks - 1);
+            }
+            tab[i] = blk;
+        }
+    };
+    if (tab_ok) fill_tab(tab_base);
+
+    // ---- issue side: STAGES-deep register pipeline ------------------------------------
+    u32x4 kr[STAGES][2][KSTEPS], vr[STAGES][2][KSTEPS];
+    DecSeg is = dec_seg_of(a, s_pref, s_bat, t0);
+
+    auto row_ptr = [&](const uint16_t* base, int64_t sb, int64_t si, int64_t sh, const DecSeg& s, int key,
+                       int blk) -> const uint16_t* {
+        if (paged) {
+            int b2 = blk;
+            if (!tab_ok) {
+                const int pidx = key / a.page;
+                b2 = min(max(a.block_table[(int64_t)s.crow * a.bt_stride + pidx], 0), a.num_blocks - 1);
+            }
+            const int inpage = a.page_shift >= 0 ? (key & (a.page - 1)) : key % a.page;
+            return base + (int64_t)b2 * sb + (int64_t)inpage * si + (int64_t)s.hk * sh;
+        }
+        if (a.cu_seqlens_k) return base + ((int64_t)a.cu_seqlens_k[s.b] + key) * si + (int64_t)s.hk * sh;
+        return base + (int64_t)s.crow * sb + (int64_t)key * si + (int64_t)s.hk * sh;
+    };
+
+    auto issue = [&](int t, u32x4 (&kk)[2][KSTEPS], u32x4 (&vv)[2][KSTEPS]) {
+        if (t >= t1) return;
+        if (t >= is.S + is.n) is = dec_seg_of(a, s_pref, s_bat, t);
+        int blk = 0;
+        if (tab_ok) {
+            if (t >= tab_base + TABN) {
+                tab_base += TABN;
+                fill_tab(tab_base);
+            }
+            blk = tab[t - tab_base];
+        }
+        const int key0 = (is.lo_tile + (t - is.S)) * KT;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int key = key0 + h * 16 + li;
+            if (key < is.sk) {
+                const uint16_t* kpr = row_ptr(kp, a.k_sb, a.k_si, a.k_sh, is, key, blk) + G * 32;
+                const uint16_t* vpr = row_ptr(vp, a.v_sb, a.v_si, a.v_sh, is, key, blk) + G * 32;
+#pragma unroll
+                for (int s = 0; s < KSTEPS; ++s) {
+                    kk[h][s] = *reinterpret_cast<const u32x4*>(kpr + s * 8);
+                    vv[h][s] = *reinterpret_cast<const u32x4*>(vpr + s * 8);
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < KSTEPS; ++s) {
+                    kk[h][s] = u32x4{0u, 0u, 0u, 0u};
+                    vv[h][s] = u32x4{0u, 0u, 0u, 0u};
+                }
+            }
+        }
+    };
+
+    // ---- compute side --------------------------------------------------------------------
+    DecSeg cs = dec_seg_of(a, s_pref, s_bat, t0);
+    u32x4 qreg[KSTEPS];
+    float slope = 0.f;
+    int qi = 0;
+    f32x4 oacc[DBLK];
+    float m_run, l_run;
+    int rows = 0;
+
+    auto begin_seg = [&](const DecSeg& s) {
+        rows = s.sq * a.g;
+        const bool ok = li < rows;
+        const int i = ok ? li / a.g : 0;
+        const int h = s.hk * a.g + (ok ? li % a.g : 0);
+        qi = i;
+        slope = (a.alibi && ok) ? a.alibi[(int64_t)s.b * a.alibi_sb + h] : 0.f;
+        const uint16_t* qrow = a.cu_seqlens_q
+                                   ? qp + ((int64_t)a.cu_seqlens_q[s.b] + i) * a.q_si + (int64_t)h * a.q_sh
+                                   : qp + (int64_t)s.b * a.q_sb + (int64_t)i * a.q_si + (int64_t)h * a.q_sh;
+#pragma unroll
+        for (int s2 = 0; s2 < KSTEPS; ++s2)
+            qreg[s2] = ok ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s2) * 8) : u32x4{0u, 0u, 0u, 0u};
+        m_run = -INFINITY;
+        l_run = 0.f;
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+
+    auto end_seg = [&](const DecSeg& s) {
+        const float lrow = wave_sum16x4(l_run);
+        const bool nonempty = lrow > 0.f;
+        const float inv = nonempty ? 1.f / lrow : 0.f;
+        const bool whole = s.S >= t0 && s.S + s.n <= t1;
+        if (li >= rows) return;
+        if (whole) {
+            const int i = li / a.g, h = s.hk * a.g + li % a.g;
+            uint16_t* op = static_cast<uint16_t*>(a.out);
+            uint16_t* orow = a.cu_seqlens_q
+                                 ? op + ((int64_t)a.cu_seqlens_q[s.b] + i) * a.o_si + (int64_t)h * a.o_sh
+                                 : op + (int64_t)s.b * a.o_sb + (int64_t)i * a.o_si + (int64_t)h * a.o_sh;
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db) {
+                f32x4 o = oacc[db] * inv;
+                uint16_t h4[4] = {f32_to_16<DT>(o[0]), f32_to_16<DT>(o[1]), f32_to_16<DT>(o[2]), f32_to_16<DT>(o[3])};
+                *reinterpret_cast<u32x2*>(orow + 16 * db + 4 * G) = __builtin_bit_cast(u32x2, h4);
+            }
+            if (G == 0) {
+                const int64_t off = a.cu_seqlens_q ? (int64_t)h * a.lse_sh + a.cu_seqlens_q[s.b] + i
+                                                   : (int64_t)s.b * a.lse_sb + (int64_t)h * a.lse_sh + i;
+                a.lse[off] = nonempty ? (m_run + fast_log2(lrow)) * kLn2 : INFINITY;
+            }
+        } else {
+            const int slot = (s.S <= t0) ? 0 : 1;  // first segment of this worker, else its last
+            const int64_t prow = (wid * 2 + slot) * 16 + li;
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db)
+                *reinterpret_cast<f32x4*>(a.part_o + prow * D + 16 * db + 4 * G) = oacc[db] * inv;
+            if (G == 0) a.part_lse[prow] = nonempty ? (m_run + fast_log2(lrow)) * kLn2 : -INFINITY;
+        }
+    };
+
+    auto compute = [&](int t, const u32x4 (&kk)[2][KSTEPS], const u32x4 (&vv)[2][KSTEPS]) {
+        const int key0 = (cs.lo_tile + (t - cs.S)) * KT;
+        // V tile -> wave-private LDS (row-major, 16-byte XOR swizzle)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int kl = h * 16 + li;
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) {
+                const int ch = G * KSTEPS + s;
+                *reinterpret_cast<u32x4*>(sv + kl * D + ((ch ^ (kl & SWZ)) << 3)) = vv[h][s];
+            }
+        }
+        // S^T = K . Q^T
+        f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+            sacc[0] = mfma16x16x32<DT>(kk[0][s], qreg[s], sacc[0]);
+            sacc[1] = mfma16x16x32<DT>(kk[1][s], qreg[s], sacc[1]);
+        }
+        // online softmax (log2 domain), row = li, keys key0 + 16h + 4G + e
+        const int sk = cs.sk, diag0 = cs.sk - cs.sq;
+        const int imax = (rows - 1) / a.g;
+        bool full = key0 + KT <= sk;
+        if (a.wl >= 0 && key0 < imax + diag0 - a.wl) full = false;
+        if (a.wr >= 0 && key0 + KT - 1 > diag0 + a.wr) full = false;
+        const bool plain = a.softcap <= 0.f && a.alibi == nullptr;
+        float x[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float sv2 = sacc[h][e];
+                float xv;
+                if (plain) {
+                    xv = sv2 * a.scale_log2;
+                } else {
+                    float y = sv2 * a.scale;
+                    if (a.softcap > 0.f) y = a.softcap * tanhf(y / a.softcap);
+                    if (a.alibi) {
+                        int dist = qi + diag0 - (key0 + h * 16 + G * 4 + e);
+                        dist = dist < 0 ? -dist : dist;
+                        y -= slope * (float)dist;
+                    }
+                    xv = y * kLog2e;
+                }
+                x[h][e] = xv;
+            }
+        if (!full) {
+            const int dg = qi + diag0;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int j = key0 + h * 16 + G * 4 + e;
+                    bool vis = j < sk;
+                    if (a.wl >= 0 && j < dg - a.wl) vis = false;
+                    if (a.wr >= 0 && j > dg + a.wr) vis = false;
+                    x[h][e] = vis ? x[h][e] : -INFINITY;
+                }
+        }
+        float tmax = fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
+                           fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
+        tmax = wave_max16x4(tmax);
+        const float m_new = fmaxf(m_run, tmax);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = fast_exp2(m_run - m_use);
+        m_run = m_new;
+        float p[2][4], psum = 0.f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                p[h][e] = fast_exp2(x[h][e] - m_use);
+                psum += p[h][e];
+            }
+        l_run = l_run * alpha + psum;
+        f32x8 p8 = {p[0][0], p[0][1], p[0][2], p[0][3], p[1][0], p[1][1], p[1][2], p[1][3]};
+        const u32x4 pk = pack8<DT>(p8);
+        // O^T += V^T . P^T with V^T from transpose reads of the LDS tile
+        const int r4 = li >> 2, c4 = li & 3;
+        const int ka = 4 * G + r4, kb = ka + 16;
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db) {
+            const int ch = 2 * db + (c4 >> 1);
+            const int off = (c4 & 1) * 4;
+            s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(sv + ka * D + ((ch ^ (ka & SWZ)) << 3) + off));
+            s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(sv + kb * D + ((ch ^ (kb & SWZ)) << 3) + off));
+            u32x2 l2 = __builtin_bit_cast(u32x2, lo4);
+            u32x2 h2 = __builtin_bit_cast(u32x2, hi4);
+            u32x4 av = {l2[0], l2[1], h2[0], h2[1]};
+            oacc[db] = mfma16x16x32<DT>(av, pk, oacc[db] * alpha);
+        }
+    };
+
+    // prologue: issue the first STAGES-1 tiles, then the first segment's q
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st) issue(t0 + st, kr[st], vr[st]);
+    begin_seg(cs);
+
+    for (int tb = t0; tb < t1; tb += STAGES) {
+#pragma unroll
+        for (int st = 0; st < STAGES; ++st) {
+            const int t = tb + st;
+            if (t < t1) {
+                issue(t + STAGES - 1, kr[(st + STAGES - 1) % STAGES], vr[(st + STAGES - 1) % STAGES]);
+                if (t >= cs.S + cs.n) {
+                    end_seg(cs);
+                    cs = dec_seg_of(a, s_pref, s_bat, t);
+                    begin_seg(cs);
+                }
+                compute(t, kr[st], vr[st]);
+            }
+        }
+    }
+    end_seg(cs);
+}
+
+// Merges the partials of segments cut by worker boundaries; writes out = 0,
+// lse = +inf for segments with no visible key. One workgroup per segment.
+template <int DT>
+__global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int workers) {
+    using namespace dec;
+    const int sig = blockIdx.x;
+    const int b = sig / a.Hk, hk = sig % a.Hk;
+    if (b >= a.B) return;
+    int sq = a.cu_seqlens_q ? a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b] : a.Sq;
+    sq = min(max(sq, 0), a.Sq);
+    const int rows = sq * a.g;
+    const int rr = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
+    if (rr >= rows) return;
+    const long long T = a.sched[a.B];
+    const int per = (a.sched[b + 1] - a.sched[b]) / a.Hk;
+    const long long S = a.sched[b] + (long long)hk * per;
+    const long long W = workers;
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    float lse = INFINITY;
+    if (per > 0) {
+        // owner(t) = the worker whose range [w*T/W, (w+1)*T/W) holds tile t;
+        // the owners of a segment are visited by hopping to owner(end of range)
+        // (workers with empty ranges own nothing and are skipped).
+        auto owner = [&](long long t) { return ((t + 1) * W - 1) / T; };
+        const long long E = S + per;
+        const long long wf = owner(S), wl = owner(E - 1);
+        if (wf == wl) return;  // one worker owned it and wrote the result
+        float m = -INFINITY;
+        for (long long w = wf;;) {
+            const int slot = (w == wf && (w * T / W) < S) ? 1 : 0;
+            m = fmaxf(m, a.part_lse[(w * 2 + slot) * 16 + rr]);
+            const long long nt = (w + 1) * T / W;
+            if (nt >= E) break;
+            w = owner(nt);
+        }
+        if (m != -INFINITY) {
+            float sum = 0.f;
+            for (long long w = wf;;) {
+                const int slot = (w == wf && (w * T / W) < S) ? 1 : 0;
+                const long long prow = (w * 2 + slot) * 16 + rr;
+                const float v = a.part_lse[prow];
+                if (v != -INFINITY) {
+                    const float wgt = fast_exp2((v - m) * kLog2e);
+                    sum += wgt;
+                    acc0 += *reinterpret_cast<const f32x4*>(a.part_o + prow * D + d0) * wgt;
+                    acc1 += *reinterpret_cast<const f32x4*>(a.part_o + prow * D + d0 + 4) * wgt;
+                }
+                const long long nt = (w + 1) * T / W;
+                if (nt >= E) break;
+                w = owner(nt);
+            }
+            const float inv = 1.f / sum;
+            acc0 *= inv;
+            acc1 *= inv;
+            lse = m + fast_log2(sum) * kLn2;
+        }
+    }
+    const int i = rr / a.g, h = hk * a.g + rr % a.g;
+    uint16_t* op = static_cast<uint16_t*>(a.out);
+    uint16_t* orow = a.cu_seqlens_q ? op + ((int64_t)a.cu_seqlens_q[b] + i) * a.o_si + (int64_t)h * a.o_sh
+                                    : op + (int64_t)b * a.o_sb + (int64_t)i * a.o_si + (int64_t)h * a.o_sh;
+    uint16_t h8[8] = {f32_to_16<DT>(acc0[0]), f32_to_16<DT>(acc0[1]), f32_to_16<DT>(acc0[2]), f32_to_16<DT>(acc0[3]),
+                      f32_to_16<DT>(acc1[0]), f32_to_16<DT>(acc1[1]), f32_to_16<DT>(acc1[2]), f32_to_16<DT>(acc1[3])};
+    *reinterpret_cast<u32x4*>(orow + d0) = __builtin_bit_cast(u32x4, h8);
+    if (d0 == 0) {
+        const int64_t off = a.cu_seqlens_q ? (int64_t)h * a.lse_sh + a.cu_seqlens_q[b] + i
+                                           : (int64_t)b * a.lse_sb + (int64_t)h * a.lse_sh + i;
+        a.lse[off] = lse;
+    }
+}
+
+constexpr int kDecodeStages = 4;
+
+int decode_workers(int cus) { return cus * dec::NWAVE; }
+
+hipError_t launch_decode(const FwdArgs& a, int dtype, int grid, hipStream_t stream) {
+    if (dtype == DT_BF16)
+        hipLaunchKernelGGL((fa_decode_kernel<DT_BF16, kDecodeStages>), dim3(grid), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((fa_decode_kernel<DT_FP16, kDecodeStages>), dim3(grid), dim3(256), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int segs = a.B * a.Hk;
+    if (dtype == DT_BF16)
+        hipLaunchKernelGGL(fa_decode_merge_kernel<DT_BF16>, dim3(segs), dim3(256), 0, stream, a, grid * dec::NWAVE);
+    else
+        hipLaunchKernelGGL(fa_decode_merge_kernel<DT_FP16>, dim3(segs), dim3(256), 0, stream, a, grid * dec::NWAVE);
+    return hipGetLastError();
+}
+
+}  // namespace fa

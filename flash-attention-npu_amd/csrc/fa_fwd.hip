@@ -215,11 +215,13 @@ __global__ void __launch_bounds__(C::NT, C::MINB) fa_fwd_kernel(FwdArgs a) {
         batch_info<BM>(a, b, bi);
         int ns, chunk;
         split_of(a, bi.hi - bi.lo, chunk_auto, ns, chunk);
+        // kv head fastest: the Hk items of one key chunk run side by side and
+        // stream the same cache rows (heads are interleaved per token in HBM)
         const int local = w - s_pref[b];
-        const int split = local % ns;
-        const int rest = local / ns;
-        const int hk = rest % a.Hk;
-        const int mt = bi.mt - 1 - rest / a.Hk;  // heaviest causal tiles first
+        const int hk = local % a.Hk;
+        const int split = (local / a.Hk) % ns;
+        const int mt_r = local / a.Hk / ns;
+        const int mt = bi.mt - 1 - mt_r;  // heaviest causal tiles first
         const bool final_out = ns == 1;
         const int crow = a.batch_idx ? min(max(a.batch_idx[b], 0), (a.block_table ? a.bt_rows : a.batch_cache) - 1) : b;
         const int g = a.g;
@@ -544,69 +546,68 @@ __global__ void __launch_bounds__(C::NT, C::MINB) fa_fwd_kernel(FwdArgs a) {
                 }
             }
         }
+
     }
 }
 
-// ---- split-KV combine ---------------------------------------------------------------
-// lse = m + ln sum_s exp(lse_s - m); O = sum_s exp(lse_s - lse) O_s
-// (CombineScale.hpp:150-194 and :248-316 of csrc/arch22/flash_attn_npu_v2).
-template <int DT, int D>
-__global__ void __launch_bounds__(256) fa_combine_kernel(CombineArgs c) {
+// Split-KV merge as its own launch: one thread per (row, 8 dims) of a split
+// row tile; the per-batch plan comes from the attention kernel's sched table.
+template <int DT, int D, int BM>
+__global__ void __launch_bounds__(256) fa_merge_kernel(FwdArgs a) {
     constexpr int DCH = D / 8;
-    const int tile = blockIdx.x;
-    const int mt_i = tile % c.mt_max;
-    const int bh = tile / c.mt_max;
-    const int hk = bh % c.Hk, b = bh / c.Hk;
-    if (b >= c.B) return;
-    const int sq = c.cu_seqlens_q ? c.cu_seqlens_q[b + 1] - c.cu_seqlens_q[b] : c.Sq;
-    const int rows = max(sq, 0) * c.g;
-    const int mt_b = (rows + c.BM - 1) / c.BM;
-    if (mt_i >= mt_b) return;
-    const int ns = c.sched[c.B + 1 + b];
-    if (ns <= 1) return;  // that tile was written by the attention kernel
-    const int base = c.sched[b] + ((mt_b - 1 - mt_i) * c.Hk + hk) * ns;
-    const int row0 = mt_i * c.BM;
-    const int nrows = min(c.BM, rows - row0);
-    uint16_t* op = static_cast<uint16_t*>(c.out);
-    for (int idx = threadIdx.x; idx < nrows * DCH; idx += blockDim.x) {
-        const int rr = idx / DCH, d0 = (idx % DCH) * 8;
-        float m = -INFINITY;
+    constexpr int RPB = 256 / DCH;                // rows per block
+    constexpr int BPT = (BM + RPB - 1) / RPB;     // blocks per tile
+    const int blk = blockIdx.x % BPT;
+    const int tile = blockIdx.x / BPT;
+    const int hk = tile % a.Hk;
+    const int bm = tile / a.Hk;
+    const int mt = bm % a.mt_max, b = bm / a.mt_max;
+    if (b >= a.B) return;
+    const int ns = a.sched[a.B + 1 + b];
+    if (ns <= 1) return;
+    int sq = a.cu_seqlens_q ? a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b] : a.Sq;
+    sq = min(max(sq, 0), a.Sq);
+    const int rows = sq * a.g;
+    const int mt_b = (rows + BM - 1) / BM;
+    if (mt >= mt_b) return;
+    const int mt_r = mt_b - 1 - mt;
+    const int rr = blk * RPB + threadIdx.x / DCH;
+    const int d0 = (threadIdx.x % DCH) * 8;
+    const int row0 = mt * BM;
+    if (rr >= min(BM, rows - row0)) return;
+    const int sst = a.Hk;  // split s of this tile is item w0 + s * Hk
+    const int w0 = a.sched[b] + mt_r * ns * a.Hk + hk;
+    float m = -INFINITY;
+    for (int s = 0; s < ns; ++s) m = fmaxf(m, a.part_lse[(int64_t)(w0 + s * sst) * BM + rr]);
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    float lse = INFINITY;
+    if (m != -INFINITY) {
+        float sum = 0.f;
         for (int s = 0; s < ns; ++s) {
-            float v = c.part_lse[(int64_t)(base + s) * c.BM + rr];
-            if (v > m && v != INFINITY) m = v;
+            const int64_t prow = (int64_t)(w0 + s * sst) * BM + rr;
+            const float wgt = fast_exp2((a.part_lse[prow] - m) * kLog2e);
+            sum += wgt;
+            acc0 += *reinterpret_cast<const f32x4*>(a.part_o + prow * D + d0) * wgt;
+            acc1 += *reinterpret_cast<const f32x4*>(a.part_o + prow * D + d0 + 4) * wgt;
         }
-        f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-        float lse = INFINITY;
-        if (m != -INFINITY) {
-            float sum = 0.f;
-            for (int s = 0; s < ns; ++s) {
-                float v = c.part_lse[(int64_t)(base + s) * c.BM + rr];
-                if (v != -INFINITY && v != INFINITY) sum += fast_exp2((v - m) * kLog2e);
-            }
-            lse = m + fast_log2(sum) * kLn2;
-            for (int s = 0; s < ns; ++s) {
-                float v = c.part_lse[(int64_t)(base + s) * c.BM + rr];
-                if (v == -INFINITY || v == INFINITY) continue;
-                float wgt = fast_exp2((v - lse) * kLog2e);
-                const float* po = c.part_o + ((int64_t)(base + s) * c.BM + rr) * D + d0;
-                acc0 += *reinterpret_cast<const f32x4*>(po) * wgt;
-                acc1 += *reinterpret_cast<const f32x4*>(po + 4) * wgt;
-            }
-        }
-        const int r = row0 + rr;
-        const int i = r / c.g, h = hk * c.g + r % c.g;
-        uint16_t* orow;
-        if (c.cu_seqlens_q) orow = op + ((int64_t)c.cu_seqlens_q[b] + i) * c.o_si + (int64_t)h * c.o_sh;
-        else orow = op + (int64_t)b * c.o_sb + (int64_t)i * c.o_si + (int64_t)h * c.o_sh;
-        uint16_t h8[8] = {f32_to_16<DT>(acc0[0]), f32_to_16<DT>(acc0[1]), f32_to_16<DT>(acc0[2]),
-                          f32_to_16<DT>(acc0[3]), f32_to_16<DT>(acc1[0]), f32_to_16<DT>(acc1[1]),
-                          f32_to_16<DT>(acc1[2]), f32_to_16<DT>(acc1[3])};
-        *reinterpret_cast<u32x4*>(orow + d0) = __builtin_bit_cast(u32x4, h8);
-        if (d0 == 0) {
-            int64_t lo_off = c.cu_seqlens_q ? (int64_t)h * c.lse_sh + c.cu_seqlens_q[b] + i
-                                            : (int64_t)b * c.lse_sb + (int64_t)h * c.lse_sh + i;
-            c.lse[lo_off] = lse;
-        }
+        const float inv = 1.f / sum;
+        acc0 *= inv;
+        acc1 *= inv;
+        lse = m + fast_log2(sum) * kLn2;
+    }
+    const int r = row0 + rr;
+    const int i = r / a.g, h = hk * a.g + r % a.g;
+    uint16_t* op = static_cast<uint16_t*>(a.out);
+    uint16_t* orow;
+    if (a.cu_seqlens_q) orow = op + ((int64_t)a.cu_seqlens_q[b] + i) * a.o_si + (int64_t)h * a.o_sh;
+    else orow = op + (int64_t)b * a.o_sb + (int64_t)i * a.o_si + (int64_t)h * a.o_sh;
+    uint16_t h8[8] = {f32_to_16<DT>(acc0[0]), f32_to_16<DT>(acc0[1]), f32_to_16<DT>(acc0[2]), f32_to_16<DT>(acc0[3]),
+                      f32_to_16<DT>(acc1[0]), f32_to_16<DT>(acc1[1]), f32_to_16<DT>(acc1[2]), f32_to_16<DT>(acc1[3])};
+    *reinterpret_cast<u32x4*>(orow + d0) = __builtin_bit_cast(u32x4, h8);
+    if (d0 == 0) {
+        int64_t lo_off = a.cu_seqlens_q ? (int64_t)h * a.lse_sh + a.cu_seqlens_q[b] + i
+                                        : (int64_t)b * a.lse_sb + (int64_t)h * a.lse_sh + i;
+        a.lse[lo_off] = lse;
     }
 }
 
@@ -654,8 +655,6 @@ __global__ void __launch_bounds__(256) fa_combine_flat_kernel(const float* __res
 
 // ---- host-side launchers (called from fa_api.cpp) -------------------------------------
 
-// decode: one 16-row tile per item, 4 waves split each 128-key tile
-template <int DT, int D> using DecodeCfg = Cfg<DT, D, 1, 4, 1, 32, 2>;
 // prefill: 128-row tile per item, 4 waves x 32 rows share each 64-key tile
 template <int DT, int D> using PrefillCfg = Cfg<DT, D, 4, 1, 2, 64, 2>;
 
@@ -665,33 +664,26 @@ static hipError_t launch_fwd_cfg(const FwdArgs& a, int grid, hipStream_t stream)
     return hipGetLastError();
 }
 
-template <int DT, int D>
-static hipError_t launch_combine_t(const CombineArgs& c, int grid, hipStream_t stream) {
-    hipLaunchKernelGGL((fa_combine_kernel<DT, D>), dim3(grid), dim3(256), 0, stream, c);
-    return hipGetLastError();
-}
 
 }  // namespace fa
 
 // Exposed to fa_api.cpp (C++ linkage inside the library).
 namespace fa {
-int fwd_tile_rows(bool decode) { return decode ? DecodeCfg<DT_BF16, 128>::BM : PrefillCfg<DT_BF16, 128>::BM; }
-int fwd_tile_keys(bool decode) { return decode ? DecodeCfg<DT_BF16, 128>::BN : PrefillCfg<DT_BF16, 128>::BN; }
+int fwd_tile_rows() { return PrefillCfg<DT_BF16, 128>::BM; }
+int fwd_tile_keys() { return PrefillCfg<DT_BF16, 128>::BN; }
 
-hipError_t launch_fwd(const FwdArgs& a, int dtype, int d, bool decode, int grid, hipStream_t stream) {
+hipError_t launch_fwd(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream) {
     if (d != 128) return hipErrorInvalidValue;
-    if (dtype == DT_BF16) {
-        return decode ? launch_fwd_cfg<DecodeCfg<DT_BF16, 128>>(a, grid, stream)
-                      : launch_fwd_cfg<PrefillCfg<DT_BF16, 128>>(a, grid, stream);
-    }
-    return decode ? launch_fwd_cfg<DecodeCfg<DT_FP16, 128>>(a, grid, stream)
-                  : launch_fwd_cfg<PrefillCfg<DT_FP16, 128>>(a, grid, stream);
+    return dtype == DT_BF16 ? launch_fwd_cfg<PrefillCfg<DT_BF16, 128>>(a, grid, stream)
+                            : launch_fwd_cfg<PrefillCfg<DT_FP16, 128>>(a, grid, stream);
 }
 
-hipError_t launch_combine(const CombineArgs& c, int dtype, int d, int grid, hipStream_t stream) {
+hipError_t launch_merge(const FwdArgs& a, int dtype, int d, hipStream_t stream) {
     if (d != 128) return hipErrorInvalidValue;
-    return dtype == DT_BF16 ? launch_combine_t<DT_BF16, 128>(c, grid, stream)
-                            : launch_combine_t<DT_FP16, 128>(c, grid, stream);
+    const int64_t grid = (int64_t)a.B * a.mt_max * a.Hk * (128 / 16);
+    if (dtype == DT_BF16) hipLaunchKernelGGL((fa_merge_kernel<DT_BF16, 128, 128>), dim3(grid), dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((fa_merge_kernel<DT_FP16, 128, 128>), dim3(grid), dim3(256), 0, stream, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_combine_flat(const float* po, const float* pl, int S, int64_t R, int Dv, void* out, int64_t ors,

@@ -49,22 +49,12 @@ struct FwdArgs {
     float* part_o;      // [item][BM][Dv] fp32
     float* part_lse;    // [item][BM]
     int* sched;         // [0..B]: item prefix, [B+1..2B]: splits per batch
+    int mt_max;         // row tiles per sequence bound
+    int page_shift;     // paged: log2(page) when page is a power of two, else -1
     int allow_split;
     int num_splits;     // > 0: forced split count
     int target_items;   // auto split: aim for about this many work items
     int min_chunk;      // auto split: smallest chunk of keys per item
-};
-
-struct CombineArgs {
-    void* out;
-    int64_t o_sb, o_si, o_sh;
-    float* lse;
-    int64_t lse_sb, lse_sh;
-    const float* part_o;
-    const float* part_lse;
-    const int* sched;
-    const int* cu_seqlens_q;
-    int B, Sq, H, Hk, g, BM, mt_max;
 };
 
 struct KvPrepArgs {

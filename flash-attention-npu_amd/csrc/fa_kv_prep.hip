@@ -30,53 +30,85 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, 
     o2 = cc + dd;
 }
 
-// Element indices of pair p (0 <= p < D/2) and whether it is rotated.
-__device__ __forceinline__ void pair_index(int p, int D, int rd, int interleaved, int& e1, int& e2, bool& rot,
-                                           int& cs_idx) {
-    if (rd > 0 && interleaved) {
-        e1 = 2 * p;
-        e2 = 2 * p + 1;
-        rot = 2 * p < rd;
-        cs_idx = p;
-    } else if (rd > 0) {
-        const int half = rd / 2;
-        if (p < half) {
-            e1 = p;
-            e2 = p + half;
-            rot = true;
-            cs_idx = p;
-        } else {
-            e1 = rd + 2 * (p - half);
-            e2 = e1 + 1;
-            rot = false;
-            cs_idx = 0;
-        }
-    } else {
-        e1 = 2 * p;
-        e2 = 2 * p + 1;
-        rot = false;
-        cs_idx = 0;
+// Rotates 4 pairs (x1[e], x2[e]) with cos/sin entries cs_idx0 .. cs_idx0+3.
+template <int DT>
+__device__ __forceinline__ void rope4(uint16_t* x1, uint16_t* x2, const uint16_t* cs, const uint16_t* sn) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float o1, o2;
+        rope_pair<DT>(f16_to_32<DT>(x1[e]), f16_to_32<DT>(x2[e]), f16_to_32<DT>(cs[e]), f16_to_32<DT>(sn[e]), o1, o2);
+        x1[e] = f32_to_16<DT>(o1);
+        x2[e] = f32_to_16<DT>(o2);
     }
 }
 
-// blockIdx.y: 0 = new keys, 1 = new values, 2 = q rotation.
+// Moves (and, for keys and q, rotates) one 8-element unit u of a head row.
+// GPT-NeoX: units u < rd/8 hold the 4 pairs (4u+e, 4u+e+rd/2); later units
+// are the untouched dims rd + 8(u - rd/8) ... Interleaved: unit u holds the
+// pairs (8u+2e, 8u+2e+1), rotated when 8u < rd. rd is a multiple of 16.
+template <int DT>
+__device__ __forceinline__ void move_unit(const uint16_t* src, uint16_t* dst, int u, int rd, int interleaved,
+                                          const uint16_t* cs_row, const uint16_t* sn_row) {
+    if (rd > 0 && !interleaved && u < rd / 8) {
+        const int half = rd / 2;
+        u32x2 a = *reinterpret_cast<const u32x2*>(src + 4 * u);
+        u32x2 b = *reinterpret_cast<const u32x2*>(src + 4 * u + half);
+        u32x2 c = *reinterpret_cast<const u32x2*>(cs_row + 4 * u);
+        u32x2 s = *reinterpret_cast<const u32x2*>(sn_row + 4 * u);
+        uint16_t x1[4], x2[4], cc[4], ss[4];
+        __builtin_memcpy(x1, &a, 8);
+        __builtin_memcpy(x2, &b, 8);
+        __builtin_memcpy(cc, &c, 8);
+        __builtin_memcpy(ss, &s, 8);
+        rope4<DT>(x1, x2, cc, ss);
+        __builtin_memcpy(&a, x1, 8);
+        __builtin_memcpy(&b, x2, 8);
+        *reinterpret_cast<u32x2*>(dst + 4 * u) = a;
+        *reinterpret_cast<u32x2*>(dst + 4 * u + half) = b;
+        return;
+    }
+    const int e0 = (rd > 0 && !interleaved) ? rd + 8 * (u - rd / 8) : 8 * u;
+    u32x4 v = *reinterpret_cast<const u32x4*>(src + e0);
+    if (rd > 0 && interleaved && e0 < rd) {
+        uint16_t x[8], x1[4], x2[4];
+        __builtin_memcpy(x, &v, 16);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x1[e] = x[2 * e];
+            x2[e] = x[2 * e + 1];
+        }
+        u32x2 c = *reinterpret_cast<const u32x2*>(cs_row + 4 * u);
+        u32x2 s = *reinterpret_cast<const u32x2*>(sn_row + 4 * u);
+        uint16_t cc[4], ss[4];
+        __builtin_memcpy(cc, &c, 8);
+        __builtin_memcpy(ss, &s, 8);
+        rope4<DT>(x1, x2, cc, ss);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x[2 * e] = x1[e];
+            x[2 * e + 1] = x2[e];
+        }
+        __builtin_memcpy(&v, x, 16);
+    }
+    *reinterpret_cast<u32x4*>(dst + e0) = v;
+}
+
+// blockIdx.y: 0 = new keys, 1 = new values, 2 = q rotation. One thread per
+// 8-element unit (16-byte loads and stores).
 template <int DT>
 __global__ void __launch_bounds__(256) fa_kv_prep_kernel(KvPrepArgs a) {
     const int which = blockIdx.y;
     const int Dw = which == 1 ? a.Dv : a.D;
-    const int pairs = Dw / 2;
+    const int units = Dw / 8;
     const int64_t nrows = which == 2 ? (int64_t)a.B * a.Sq * a.H : (int64_t)a.B * a.S_new * a.Hk;
-    const int64_t total = nrows * pairs;
+    const int64_t total = nrows * units;
     const uint16_t* cs = static_cast<const uint16_t*>(a.cos);
     const uint16_t* sn = static_cast<const uint16_t*>(a.sin);
+    const int rd = which == 1 ? 0 : a.rotary_dim;
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (int64_t)gridDim.x * blockDim.x) {
-        const int p = (int)(idx % pairs);
-        const int64_t row = idx / pairs;
-        int e1, e2, cs_idx;
-        bool rot;
-        const int rd = which == 1 ? 0 : a.rotary_dim;
-        pair_index(p, Dw, rd, a.interleaved, e1, e2, rot, cs_idx);
+        const int u = (int)(idx % units);
+        const int64_t row = idx / units;
         if (which == 2) {
             const int h = (int)(row % a.H);
             const int i = (int)((row / a.H) % a.Sq);
@@ -84,19 +116,9 @@ __global__ void __launch_bounds__(256) fa_kv_prep_kernel(KvPrepArgs a) {
             const uint16_t* src = static_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_sb + (int64_t)i * a.q_si +
                                   (int64_t)h * a.q_sh;
             uint16_t* dst = static_cast<uint16_t*>(a.q_out) + (((int64_t)b * a.Sq + i) * a.H + h) * a.D;
-            uint16_t x1 = src[e1], x2 = src[e2];
-            if (rot) {
-                int pos = (a.seqlens ? a.seqlens[b] : 0) + (a.q_same_pos ? 0 : i);
-                pos = min(max(pos, 0), a.seqlen_ro - 1);
-                float c = f16_to_32<DT>(cs[(int64_t)pos * a.cs_stride + cs_idx]);
-                float s = f16_to_32<DT>(sn[(int64_t)pos * a.cs_stride + cs_idx]);
-                float o1, o2;
-                rope_pair<DT>(f16_to_32<DT>(x1), f16_to_32<DT>(x2), c, s, o1, o2);
-                x1 = f32_to_16<DT>(o1);
-                x2 = f32_to_16<DT>(o2);
-            }
-            dst[e1] = x1;
-            dst[e2] = x2;
+            int pos = (a.seqlens ? a.seqlens[b] : 0) + (a.q_same_pos ? 0 : i);
+            pos = min(max(pos, 0), a.seqlen_ro - 1);
+            move_unit<DT>(src, dst, u, rd, a.interleaved, cs + (int64_t)pos * a.cs_stride, sn + (int64_t)pos * a.cs_stride);
             continue;
         }
         const int h = (int)(row % a.Hk);
@@ -125,18 +147,9 @@ __global__ void __launch_bounds__(256) fa_kv_prep_kernel(KvPrepArgs a) {
         else
             src = static_cast<const uint16_t*>(a.v_new) + (int64_t)b * a.vn_sb + (int64_t)t * a.vn_si +
                   (int64_t)h * a.vn_sh;
-        uint16_t x1 = src[e1], x2 = src[e2];
-        if (rot) {
-            const int pos = min(j, a.seqlen_ro - 1);
-            float c = f16_to_32<DT>(cs[(int64_t)pos * a.cs_stride + cs_idx]);
-            float s = f16_to_32<DT>(sn[(int64_t)pos * a.cs_stride + cs_idx]);
-            float o1, o2;
-            rope_pair<DT>(f16_to_32<DT>(x1), f16_to_32<DT>(x2), c, s, o1, o2);
-            x1 = f32_to_16<DT>(o1);
-            x2 = f32_to_16<DT>(o2);
-        }
-        dst[e1] = x1;
-        dst[e2] = x2;
+        const int pos = min(j, a.seqlen_ro - 1);
+        move_unit<DT>(src, dst, u, rd, a.interleaved, rd ? cs + (int64_t)pos * a.cs_stride : nullptr,
+                      rd ? sn + (int64_t)pos * a.cs_stride : nullptr);
     }
 }
 
@@ -145,7 +158,7 @@ hipError_t launch_kv_prep(const KvPrepArgs& a, int dtype, hipStream_t stream) {
     int64_t rows_kv = (int64_t)a.B * a.S_new * a.Hk;
     int64_t rows_q = a.q_out ? (int64_t)a.B * a.Sq * a.H : 0;
     int64_t mx = rows_kv > rows_q ? rows_kv : rows_q;
-    int64_t work = mx * (a.D > a.Dv ? a.D : a.Dv) / 2;
+    int64_t work = mx * (a.D > a.Dv ? a.D : a.Dv) / 8;
     int grid = (int)((work + 255) / 256);
     if (grid > 8192) grid = 8192;
     if (grid < 1) grid = 1;

@@ -46,6 +46,7 @@ class FwdParams(ctypes.Structure):
         ("softmax_scale", ctypes.c_float), ("softcap", ctypes.c_float), ("dropout_p", ctypes.c_float),
         ("is_causal", _i32), ("window_size_left", _i32), ("window_size_right", _i32), ("num_splits", _i32),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("stage_events", _vp),
     ]
 
 

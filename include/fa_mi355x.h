@@ -122,6 +122,11 @@ typedef struct fa_fwd_params {
 
     void* workspace;
     size_t workspace_bytes;
+
+    /* Optional profiling hook: NULL, or 4 hipEvent_t handles recorded on
+       `stream` before the KV append, before the attention kernel, before the
+       split-KV combine and after the last kernel of the call. */
+    void* const* stage_events;
 } fa_fwd_params;
 
 /* Library / ABI version. */

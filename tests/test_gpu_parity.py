@@ -183,3 +183,157 @@ def test_v3_kvcache_paged():
     print("case v3 kvcache paged", flush=True)
     run_kvcache(3, 2, 16, 4, 128, torch.float16, 0, [100, 700, 1300], s_new=2, page=64, causal=True, seed=9,
                 api="v3")
+
+
+# ---- split-KV merge: repeated calls reuse the self-clearing arrival counters -----------------
+def test_split_counters_reset_across_calls():
+    print("case repeated split calls", flush=True)
+    for rep in range(3):
+        run_kvcache(5, 1, 32, 8, 128, torch.bfloat16, 4096, [4000, 100, 2500, 3000, 1], s_new=1, causal=True,
+                    num_splits=0, seed=20)
+
+
+def test_prefill_shape_split_small_batch():
+    # 64 query rows x g=4 -> the 128-row prefill kernel, few tiles -> auto split
+    print("case prefill-shape split", flush=True)
+    run_kvcache(1, 64, 32, 8, 128, torch.bfloat16, 4096, [3900], s_new=0, causal=True, seed=21)
+
+
+def test_forced_split_window_empty_splits():
+    print("case forced split with window", flush=True)
+    run_kvcache(3, 2, 16, 4, 128, torch.float16, 0, [3000, 5000, 700], s_new=2, page=128, causal=True,
+                window=(300, 0), num_splits=7, seed=22)
+
+
+def test_contiguous_cache_batch_idx_append():
+    print("case contiguous cache_batch_idx", flush=True)
+    run_kvcache(4, 3, 16, 4, 128, torch.bfloat16, 1024, [10, 500, 900, 0], s_new=3, causal=True, batch_idx=True,
+                seed=23)
+
+
+def test_noncausal_decode_rotary_same_position():
+    # not causal and not local: every q row is rotated at cache_seqlens[b]
+    print("case non-causal rotary", flush=True)
+    run_kvcache(2, 3, 16, 4, 128, torch.bfloat16, 512, [100, 200], s_new=3, rotary="partial", causal=False, seed=24)
+
+
+# ---- varlen ---------------------------------------------------------------------------------
+@pytest.mark.parametrize("causal", [False, True])
+def test_varlen(causal):
+    import flash_attn_npu_v2
+    print(f"case varlen causal={causal}", flush=True)
+    g = _gen(30)
+    dtype = torch.bfloat16
+    H, Hk, D = 8, 2, 128
+    lq = [37, 1, 300, 128]
+    lk = [37, 90, 300, 1000]
+    cq = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
+    ck = np.concatenate([[0], np.cumsum(lk)]).astype(np.int32)
+    q = randn((cq[-1], H, D), dtype, g, "cpu")
+    k = randn((ck[-1], Hk, D), dtype, g, "cpu")
+    v = randn((ck[-1], Hk, D), dtype, g, "cpu")
+    ref_out, ref_lse = orc.attention(bits(q).reshape(q.shape), bits(k).reshape(k.shape), bits(v).reshape(v.shape),
+                                     dtype=odt(dtype), scale=D ** -0.5, causal=causal, cu_seqlens_q=cq,
+                                     cu_seqlens_k=ck, max_seqlen_q=max(lq), nthreads=NT)
+    out, lse, _ = flash_attn_npu_v2.flash_attn_varlen_func(
+        q.to(DEV), k.to(DEV), v.to(DEV), torch.from_numpy(cq).to(DEV), torch.from_numpy(ck).to(DEV), max(lq),
+        max(lk), causal=causal, return_attn_probs=True)
+    torch.cuda.synchronize()
+    assert_close_out(out, ref_out, dtype)
+    assert_close_lse(lse, ref_lse)
+
+
+def test_v3_varlen_q_paged_kvcache():
+    import flash_attn_npu_v3
+    print("case v3 TND q against paged cache", flush=True)
+    g = _gen(31)
+    dtype = torch.float16
+    H, Hk, D, page = 8, 2, 128, 64
+    lq = [3, 1, 7]
+    L = [200, 64, 1000]
+    need = [(x + page - 1) // page for x in L]
+    nb = sum(need) + 3
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    bt = torch.zeros((3, max(need)), dtype=torch.int32)
+    o = 0
+    for b in range(3):
+        bt[b, :need[b]] = perm[o:o + need[b]]
+        o += need[b]
+    cq = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
+    q = randn((cq[-1], H, D), dtype, g, "cpu")
+    kc = randn((nb, page, Hk, D), dtype, g, "cpu")
+    vc = randn((nb, page, Hk, D), dtype, g, "cpu")
+    ref_out, ref_lse = orc.attention(bits(q).reshape(q.shape), bits(kc).reshape(kc.shape),
+                                     bits(vc).reshape(vc.shape), dtype=odt(dtype), scale=D ** -0.5, causal=True,
+                                     cu_seqlens_q=cq, max_seqlen_q=max(lq), seqlens_k=np.array(L, np.int32),
+                                     block_table=bt.numpy(), nthreads=NT)
+    out, lse, *_ = flash_attn_npu_v3.flash_attn_with_kvcache(
+        q.to(DEV), kc.to(DEV), vc.to(DEV), cache_seqlens=torch.tensor(L, dtype=torch.int32, device=DEV),
+        page_table=bt.to(DEV), cu_seqlens_q=torch.from_numpy(cq).to(DEV), max_seqlen_q=max(lq), causal=True,
+        return_softmax_lse=True)
+    torch.cuda.synchronize()
+    assert_close_out(out, ref_out, dtype)
+    assert_close_lse(lse, ref_lse)
+
+
+# ---- flash_attn_combine ----------------------------------------------------------------------
+def test_flash_attn_combine():
+    import flash_attn_npu_v3
+    print("case flash_attn_combine", flush=True)
+    g = _gen(40)
+    S, B, Sq, H, Dv = 5, 2, 3, 4, 128
+    op = torch.randn((S, B, Sq, H, Dv), generator=g)
+    lp = torch.randn((S, B, Sq, H), generator=g) * 3
+    lp[1, 0, 0, 0] = -float("inf")          # an empty split
+    lp[:, 1, 2, 3] = -float("inf")          # a row with no keys at all
+    ref_o, ref_l = orc.combine(op.reshape(S, -1, Dv).numpy(), lp.reshape(S, -1).numpy())
+    out, lse = flash_attn_npu_v3.flash_attn_combine(op.to(DEV), lp.to(DEV), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(out.cpu().reshape(-1, Dv).numpy(), ref_o, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(lse.cpu().reshape(-1).numpy(), ref_l, rtol=1e-5, atol=1e-5)
+
+
+# ---- direct C-ABI call (ctypes), no torch operator in between -----------------------------------
+def test_capi_direct_dense():
+    import ctypes
+    from fa_mi355x import capi
+    print("case C ABI direct", flush=True)
+    g = _gen(50)
+    dtype = torch.float16
+    B, S, H, D = 1, 257, 4, 128
+    q, k, v = (randn((B, S, H, D), dtype, g, "cpu") for _ in range(3))
+    ref_out, ref_lse = orc.attention(bits(q).reshape(q.shape), bits(k).reshape(k.shape), bits(v).reshape(v.shape),
+                                     dtype=odt(dtype), scale=D ** -0.5, causal=True, nthreads=NT)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    out = torch.empty_like(qd)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=DEV)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    p = capi.new_params(dtype=capi.FA_DTYPE_FP16, batch=B, seqlen_q=S, nheads=H, nheads_k=H, headdim=D,
+                        headdim_v=D, seqlen_k=S, batch_cache=B, q=P(qd), q_batch_stride=qd.stride(0),
+                        q_row_stride=qd.stride(1), q_head_stride=qd.stride(2), k=P(kd), k_batch_stride=kd.stride(0),
+                        k_row_stride=kd.stride(1), k_head_stride=kd.stride(2), v=P(vd), v_batch_stride=vd.stride(0),
+                        v_row_stride=vd.stride(1), v_head_stride=vd.stride(2), out=P(out),
+                        out_batch_stride=out.stride(0), out_row_stride=out.stride(1), out_head_stride=out.stride(2),
+                        softmax_lse=P(lse), softmax_scale=D ** -0.5, is_causal=1)
+    st, nbytes = capi.workspace_size(p, capi.FA_KIND_DENSE)
+    assert st == capi.FA_OK, capi.last_error()
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=DEV)
+    p.workspace, p.workspace_bytes = P(ws), ws.numel()
+    st = capi.forward(p, capi.FA_KIND_DENSE, torch.cuda.current_stream().cuda_stream)
+    assert st == capi.FA_OK, capi.last_error()
+    torch.cuda.synchronize()
+    assert_close_out(out, ref_out, dtype)
+    assert_close_lse(lse, ref_lse)
+
+
+def test_errors_raise():
+    import flash_attn_npu_v2
+    print("case error paths", flush=True)
+    q = torch.zeros((1, 4, 8, 128), dtype=torch.bfloat16, device=DEV)
+    k = torch.zeros((1, 4, 3, 128), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="divide"):
+        flash_attn_npu_v2.flash_attn_func(q, k, k)
+    with pytest.raises(RuntimeError, match="dropout"):
+        flash_attn_npu_v2.flash_attn_func(q, q, q, dropout_p=0.1)
+    with pytest.raises(RuntimeError):
+        flash_attn_npu_v2.flash_attn_func(q.float(), q.float(), q.float())
