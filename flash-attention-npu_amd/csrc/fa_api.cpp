@@ -252,7 +252,10 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
         if (p->stage_events && p->stage_events[i]) (void)hipEventRecord(static_cast<hipEvent_t>(p->stage_events[i]), stream);
     };
     mark(0);
-    if (kind == FA_KIND_KVCACHE && p->k_new) {
+    // Decode without rotary appends inside the attention kernel; otherwise the
+    // append (and rotary) runs as its own launch first.
+    const bool fused_append = kind == FA_KIND_KVCACHE && p->k_new && pl.decode && !pl.rotary;
+    if (kind == FA_KIND_KVCACHE && p->k_new && !fused_append) {
         fa::KvPrepArgs k{};
         k.k_new = p->k_new;
         k.kn_sb = p->knew_batch_stride;
@@ -352,6 +355,16 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
     a.Hk = p->nheads_k;
     a.g = pl.g;
     a.seqlen_new = (kind == FA_KIND_KVCACHE && p->k_new) ? p->seqlen_new : 0;
+    if (fused_append) {
+        a.k_new = p->k_new;
+        a.kn_sb = p->knew_batch_stride;
+        a.kn_si = p->knew_row_stride;
+        a.kn_sh = p->knew_head_stride;
+        a.v_new = p->v_new;
+        a.vn_sb = p->vnew_batch_stride;
+        a.vn_si = p->vnew_row_stride;
+        a.vn_sh = p->vnew_head_stride;
+    }
     // window normalisation (flash_api.cpp:483-494): the seqlen-dependent rules
     // leave the mask unchanged, causal forces the right edge to the diagonal
     int wl = p->window_size_left < 0 ? -1 : p->window_size_left;

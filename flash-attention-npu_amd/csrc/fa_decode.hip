@@ -85,7 +85,8 @@ __device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref
     return s;
 }
 
-template <int DT, int STAGES>
+// BIAS: softcap or ALiBi present; FUSE: append k_new/v_new in this kernel.
+template <int DT, int STAGES, bool BIAS, bool FUSE>
 __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     using namespace dec;
     __shared__ int s_pref[MAXB + 1];
@@ -161,6 +162,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
 
     // ---- issue side: STAGES-deep register pipeline ------------------------------------
     u32x4 kr[STAGES][2][KSTEPS], vr[STAGES][2][KSTEPS];
+    int bk[STAGES];  // paged block id of each in-flight tile
     DecSeg is = dec_seg_of(a, s_pref, s_bat, t0);
 
     auto row_ptr = [&](const uint16_t* base, int64_t sb, int64_t si, int64_t sh, const DecSeg& s, int key,
@@ -178,10 +180,17 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         return base + (int64_t)s.crow * sb + (int64_t)key * si + (int64_t)s.hk * sh;
     };
 
-    auto issue = [&](int t, u32x4 (&kk)[2][KSTEPS], u32x4 (&vv)[2][KSTEPS]) {
+    // With a fused append, keys >= sk - seqlen_new come from k_new / v_new; the
+    // worker that owns their tile also writes them into the cache (each tile
+    // has exactly one owner, and no other tile reads those positions).
+    constexpr bool fuse = FUSE;
+    const uint16_t* knp = static_cast<const uint16_t*>(a.k_new);
+    const uint16_t* vnp = static_cast<const uint16_t*>(a.v_new);
+
+    auto issue = [&](int t, u32x4 (&kk)[2][KSTEPS], u32x4 (&vv)[2][KSTEPS], int& blk) {
         if (t >= t1) return;
         if (t >= is.S + is.n) is = dec_seg_of(a, s_pref, s_bat, t);
-        int blk = 0;
+        blk = 0;
         if (tab_ok) {
             if (t >= tab_base + TABN) {
                 tab_base += TABN;
@@ -190,12 +199,21 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             blk = tab[t - tab_base];
         }
         const int key0 = (is.lo_tile + (t - is.S)) * KT;
+        const int first_new = fuse ? is.sk - a.seqlen_new : 0x7fffffff;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int key = key0 + h * 16 + li;
             if (key < is.sk) {
-                const uint16_t* kpr = row_ptr(kp, a.k_sb, a.k_si, a.k_sh, is, key, blk) + G * 32;
-                const uint16_t* vpr = row_ptr(vp, a.v_sb, a.v_si, a.v_sh, is, key, blk) + G * 32;
+                const uint16_t* kpr;
+                const uint16_t* vpr;
+                if (key >= first_new) {
+                    const int tn = key - first_new;
+                    kpr = knp + (int64_t)is.b * a.kn_sb + (int64_t)tn * a.kn_si + (int64_t)is.hk * a.kn_sh + G * 32;
+                    vpr = vnp + (int64_t)is.b * a.vn_sb + (int64_t)tn * a.vn_si + (int64_t)is.hk * a.vn_sh + G * 32;
+                } else {
+                    kpr = row_ptr(kp, a.k_sb, a.k_si, a.k_sh, is, key, blk) + G * 32;
+                    vpr = row_ptr(vp, a.v_sb, a.v_si, a.v_sh, is, key, blk) + G * 32;
+                }
 #pragma unroll
                 for (int s = 0; s < KSTEPS; ++s) {
                     kk[h][s] = *reinterpret_cast<const u32x4*>(kpr + s * 8);
@@ -272,8 +290,27 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         }
     };
 
-    auto compute = [&](int t, const u32x4 (&kk)[2][KSTEPS], const u32x4 (&vv)[2][KSTEPS]) {
+    auto compute = [&](int t, const u32x4 (&kk)[2][KSTEPS], const u32x4 (&vv)[2][KSTEPS], int blk) {
         const int key0 = (cs.lo_tile + (t - cs.S)) * KT;
+        if (fuse && key0 + KT > cs.sk - a.seqlen_new) {
+            // this tile holds appended tokens: write them into the cache
+            const int first_new = cs.sk - a.seqlen_new;
+            uint16_t* kc = const_cast<uint16_t*>(kp);
+            uint16_t* vc = const_cast<uint16_t*>(vp);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int key = key0 + h * 16 + li;
+                if (key >= first_new && key < cs.sk) {
+                    uint16_t* kd = const_cast<uint16_t*>(row_ptr(kc, a.k_sb, a.k_si, a.k_sh, cs, key, blk)) + G * 32;
+                    uint16_t* vd = const_cast<uint16_t*>(row_ptr(vc, a.v_sb, a.v_si, a.v_sh, cs, key, blk)) + G * 32;
+#pragma unroll
+                    for (int s = 0; s < KSTEPS; ++s) {
+                        *reinterpret_cast<u32x4*>(kd + s * 8) = kk[h][s];
+                        *reinterpret_cast<u32x4*>(vd + s * 8) = vv[h][s];
+                    }
+                }
+            }
+        }
         // V tile -> wave-private LDS (row-major, 16-byte XOR swizzle)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -297,7 +334,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         bool full = key0 + KT <= sk;
         if (a.wl >= 0 && key0 < imax + diag0 - a.wl) full = false;
         if (a.wr >= 0 && key0 + KT - 1 > diag0 + a.wr) full = false;
-        const bool plain = a.softcap <= 0.f && a.alibi == nullptr;
+        constexpr bool plain = !BIAS;
         float x[2][4];
 #pragma unroll
         for (int h = 0; h < 2; ++h)
@@ -368,7 +405,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
 
     // prologue: issue the first STAGES-1 tiles, then the first segment's q
 #pragma unroll
-    for (int st = 0; st < STAGES - 1; ++st) issue(t0 + st, kr[st], vr[st]);
+    for (int st = 0; st < STAGES - 1; ++st) issue(t0 + st, kr[st], vr[st], bk[st]);
     begin_seg(cs);
 
     for (int tb = t0; tb < t1; tb += STAGES) {
@@ -376,13 +413,14 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         for (int st = 0; st < STAGES; ++st) {
             const int t = tb + st;
             if (t < t1) {
-                issue(t + STAGES - 1, kr[(st + STAGES - 1) % STAGES], vr[(st + STAGES - 1) % STAGES]);
+                issue(t + STAGES - 1, kr[(st + STAGES - 1) % STAGES], vr[(st + STAGES - 1) % STAGES],
+                      bk[(st + STAGES - 1) % STAGES]);
                 if (t >= cs.S + cs.n) {
                     end_seg(cs);
                     cs = dec_seg_of(a, s_pref, s_bat, t);
                     begin_seg(cs);
                 }
-                compute(t, kr[st], vr[st]);
+                compute(t, kr[st], vr[st], bk[st]);
             }
         }
     }
@@ -410,36 +448,33 @@ __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int wor
     float lse = INFINITY;
     if (per > 0) {
         // owner(t) = the worker whose range [w*T/W, (w+1)*T/W) holds tile t;
-        // the owners of a segment are visited by hopping to owner(end of range)
-        // (workers with empty ranges own nothing and are skipped).
+        // workers with empty ranges (T < W) own nothing and are skipped by
+        // hopping to owner(end of range). One pass with a running maximum.
         auto owner = [&](long long t) { return ((t + 1) * W - 1) / T; };
         const long long E = S + per;
         const long long wf = owner(S), wl = owner(E - 1);
         if (wf == wl) return;  // one worker owned it and wrote the result
-        float m = -INFINITY;
-        for (long long w = wf;;) {
-            const int slot = (w == wf && (w * T / W) < S) ? 1 : 0;
-            m = fmaxf(m, a.part_lse[(w * 2 + slot) * 16 + rr]);
-            const long long nt = (w + 1) * T / W;
-            if (nt >= E) break;
-            w = owner(nt);
+        float m = -INFINITY, sum = 0.f;
+        long long w = wf;
+        int slot = (wf * T / W) < S ? 1 : 0;
+        while (true) {
+            const long long prow = (w * 2 + slot) * 16 + rr;
+            const float v = a.part_lse[prow];
+            if (v != -INFINITY) {
+                const f32x4 o0 = *reinterpret_cast<const f32x4*>(a.part_o + prow * D + d0);
+                const f32x4 o1 = *reinterpret_cast<const f32x4*>(a.part_o + prow * D + d0 + 4);
+                const float mn = fmaxf(m, v);
+                const float sc = fast_exp2((m - mn) * kLog2e), wgt = fast_exp2((v - mn) * kLog2e);
+                acc0 = acc0 * sc + o0 * wgt;
+                acc1 = acc1 * sc + o1 * wgt;
+                sum = sum * sc + wgt;
+                m = mn;
+            }
+            slot = 0;
+            if (w == wl) break;
+            w = (T >= W) ? w + 1 : owner((w + 1) * T / W);
         }
         if (m != -INFINITY) {
-            float sum = 0.f;
-            for (long long w = wf;;) {
-                const int slot = (w == wf && (w * T / W) < S) ? 1 : 0;
-                const long long prow = (w * 2 + slot) * 16 + rr;
-                const float v = a.part_lse[prow];
-                if (v != -INFINITY) {
-                    const float wgt = fast_exp2((v - m) * kLog2e);
-                    sum += wgt;
-                    acc0 += *reinterpret_cast<const f32x4*>(a.part_o + prow * D + d0) * wgt;
-                    acc1 += *reinterpret_cast<const f32x4*>(a.part_o + prow * D + d0 + 4) * wgt;
-                }
-                const long long nt = (w + 1) * T / W;
-                if (nt >= E) break;
-                w = owner(nt);
-            }
             const float inv = 1.f / sum;
             acc0 *= inv;
             acc1 *= inv;
@@ -460,15 +495,26 @@ __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int wor
     }
 }
 
-constexpr int kDecodeStages = 4;
+constexpr int kDecodeStages = 3;
 
 int decode_workers(int cus) { return cus * dec::NWAVE; }
 
+template <int DT>
+static void launch_decode_t(const FwdArgs& a, int grid, hipStream_t stream) {
+    const bool bias = a.softcap > 0.f || a.alibi != nullptr;
+    const bool fuse = a.k_new != nullptr;
+    if (bias) {
+        if (fuse) hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, true, true>), dim3(grid), dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, true, false>), dim3(grid), dim3(256), 0, stream, a);
+    } else {
+        if (fuse) hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, false, true>), dim3(grid), dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, false, false>), dim3(grid), dim3(256), 0, stream, a);
+    }
+}
+
 hipError_t launch_decode(const FwdArgs& a, int dtype, int grid, hipStream_t stream) {
-    if (dtype == DT_BF16)
-        hipLaunchKernelGGL((fa_decode_kernel<DT_BF16, kDecodeStages>), dim3(grid), dim3(256), 0, stream, a);
-    else
-        hipLaunchKernelGGL((fa_decode_kernel<DT_FP16, kDecodeStages>), dim3(grid), dim3(256), 0, stream, a);
+    if (dtype == DT_BF16) launch_decode_t<DT_BF16>(a, grid, stream);
+    else launch_decode_t<DT_FP16>(a, grid, stream);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int segs = a.B * a.Hk;

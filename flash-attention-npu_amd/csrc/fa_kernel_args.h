@@ -55,6 +55,11 @@ struct FwdArgs {
     int num_splits;     // > 0: forced split count
     int target_items;   // auto split: aim for about this many work items
     int min_chunk;      // auto split: smallest chunk of keys per item
+    // decode with a fused append (no rotary): the new tokens (B, S_new, Hk, D)
+    const void* k_new;
+    int64_t kn_sb, kn_si, kn_sh;
+    const void* v_new;
+    int64_t vn_sb, vn_si, vn_sh;
 };
 
 struct KvPrepArgs {
