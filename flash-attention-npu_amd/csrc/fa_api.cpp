@@ -207,7 +207,7 @@ void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
         const int occ = 2;  // prefill workgroups per CU
         const int64_t base_bound = (int64_t)p->batch * p->nheads_k * pl.mt_max;
         pl.workers = 0;
-        pl.target_items = 4 * cus;
+        pl.target_items = 2 * cus;
         pl.min_chunk = 2 * pl.BN;
         if (p->num_splits == 1) pl.allow_split = false;
         else if (p->num_splits > 1) pl.allow_split = true;

@@ -85,8 +85,9 @@ __device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref
     return s;
 }
 
-// BIAS: softcap or ALiBi present; FUSE: append k_new/v_new in this kernel.
-template <int DT, int STAGES, bool BIAS, bool FUSE>
+// BIAS: softcap or ALiBi present; FUSE: append k_new/v_new in this kernel;
+// LAYOUT: 0 = batch-strided cache, 1 = paged with page % 32 == 0, 2 = any.
+template <int DT, int STAGES, bool BIAS, bool FUSE, int LAYOUT>
 __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     using namespace dec;
     __shared__ int s_pref[MAXB + 1];
@@ -140,8 +141,8 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     const uint16_t* vp = static_cast<const uint16_t*>(a.v);
     uint16_t* sv = s_v[wave];
     int* tab = s_tab[wave];
-    const bool paged = a.block_table != nullptr;
-    const bool tab_ok = paged && (a.page % KT) == 0;
+    const bool paged = LAYOUT == 1 || (LAYOUT == 2 && a.block_table != nullptr);
+    const bool tab_ok = LAYOUT == 1;
     int tab_base = t0;
 
     auto fill_tab = [&](int base) {
@@ -176,7 +177,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             const int inpage = a.page_shift >= 0 ? (key & (a.page - 1)) : key % a.page;
             return base + (int64_t)b2 * sb + (int64_t)inpage * si + (int64_t)s.hk * sh;
         }
-        if (a.cu_seqlens_k) return base + ((int64_t)a.cu_seqlens_k[s.b] + key) * si + (int64_t)s.hk * sh;
+        if (LAYOUT == 2 && a.cu_seqlens_k) return base + ((int64_t)a.cu_seqlens_k[s.b] + key) * si + (int64_t)s.hk * sh;
         return base + (int64_t)s.crow * sb + (int64_t)key * si + (int64_t)s.hk * sh;
     };
 
@@ -499,17 +500,24 @@ constexpr int kDecodeStages = 3;
 
 int decode_workers(int cus) { return cus * dec::NWAVE; }
 
-template <int DT>
-static void launch_decode_t(const FwdArgs& a, int grid, hipStream_t stream) {
+template <int DT, int LAYOUT>
+static void launch_decode_l(const FwdArgs& a, int grid, hipStream_t stream) {
     const bool bias = a.softcap > 0.f || a.alibi != nullptr;
     const bool fuse = a.k_new != nullptr;
     if (bias) {
-        if (fuse) hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, true, true>), dim3(grid), dim3(256), 0, stream, a);
-        else hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, true, false>), dim3(grid), dim3(256), 0, stream, a);
+        if (fuse) hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, true, true, LAYOUT>), dim3(grid), dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, true, false, LAYOUT>), dim3(grid), dim3(256), 0, stream, a);
     } else {
-        if (fuse) hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, false, true>), dim3(grid), dim3(256), 0, stream, a);
-        else hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, false, false>), dim3(grid), dim3(256), 0, stream, a);
+        if (fuse) hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, false, true, LAYOUT>), dim3(grid), dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, false, false, LAYOUT>), dim3(grid), dim3(256), 0, stream, a);
     }
+}
+
+template <int DT>
+static void launch_decode_t(const FwdArgs& a, int grid, hipStream_t stream) {
+    if (a.block_table && (a.page % dec::KT) == 0) launch_decode_l<DT, 1>(a, grid, stream);
+    else if (a.block_table || a.cu_seqlens_k) launch_decode_l<DT, 2>(a, grid, stream);
+    else launch_decode_l<DT, 0>(a, grid, stream);
 }
 
 hipError_t launch_decode(const FwdArgs& a, int dtype, int grid, hipStream_t stream) {
