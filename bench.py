@@ -293,6 +293,21 @@ def cpu_baseline(c, torch):
                       f"{nthreads} OpenMP threads, {reps} reps, {dt * 1e3:.1f} ms/rep"}
 
 
+TRAFFIC_PROFILE = "profiles/fa_decode_kernel_hbm_traffic.txt"
+
+
+def measured_traffic(cfg):
+    """HBM bytes per launch of the decode kernel on `cfg`, as measured by the two
+    rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) summarised in TRAFFIC_PROFILE
+    (scaled by the plain-copy calibration recorded there); None if absent."""
+    import re
+    path = os.path.join(REPO, TRAFFIC_PROFILE)
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"^traffic_bytes_per_launch\[%s\]\s*=\s*(\d+)" % cfg, open(path).read(), re.M)
+    return int(m.group(1)) if m else None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -300,6 +315,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="c2,c3,c4,c5")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 3 plain device copies of 1 GiB (reference for rocprof FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -343,7 +360,15 @@ def main():
             del c
             torch.cuda.empty_cache()
 
+    if args.copy_calibration:
+        src = torch.ones(1 << 28, dtype=torch.int32, device=dev)  # 1 GiB read, 1 GiB written
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     c2 = results["c2"]
+    traffic = measured_traffic("c2")
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(cases["c2"], torch)
@@ -364,8 +389,10 @@ def main():
         "config": {"workload": "BASELINE config 2: " + c2["workload"], "batch": 32, "nheads": 32, "nheads_k": 8,
                    "headdim": 128, "seqlen_cache": 8192, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(c2["attn_tbps"] * 1e3, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(c2["attn_frac_hbm"], 4), "traffic": None,
-                     "kernel": "fa_fwd_kernel (decode config)", "kernel_us": round(c2["attn_us"], 2)},
+                     "unit": "GB/s", "frac": round(c2["attn_frac_hbm"], 4), "traffic": traffic,
+                     "kernel": "fa_decode_kernel", "kernel_us": round(c2["attn_us"], 2),
+                     "algorithmic_bytes": c2["attn_bytes"],
+                     "traffic_source": TRAFFIC_PROFILE if traffic is not None else None},
         "cpu_baseline": cpu,
         "configs": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in results.items()},

@@ -28,6 +28,7 @@ int decode_workers(int cus);
 hipError_t launch_fwd(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream);
 hipError_t launch_merge(const FwdArgs& a, int dtype, int d, hipStream_t stream);
 hipError_t launch_decode(const FwdArgs& a, int dtype, int grid, hipStream_t stream);
+hipError_t launch_decode_merge(const FwdArgs& a, int dtype, int grid, hipStream_t stream);
 hipError_t launch_combine_flat(const float* po, const float* pl, int S, int64_t R, int Dv, void* out, int64_t ors,
                                int out_dtype, float* lse, hipStream_t stream);
 hipError_t launch_kv_prep(const KvPrepArgs& a, int dtype, hipStream_t stream);
@@ -397,7 +398,10 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
                              : fa::launch_fwd(a, p->dtype, p->headdim, pl.grid, stream);
     if (e != hipSuccess) return fail(FA_EHIP, "attention launch failed: %s", hipGetErrorString(e));
     mark(2);
-    if (!pl.decode && pl.allow_split) {
+    if (pl.decode) {
+        hipError_t em = fa::launch_decode_merge(a, p->dtype, pl.grid, stream);
+        if (em != hipSuccess) return fail(FA_EHIP, "merge launch failed: %s", hipGetErrorString(em));
+    } else if (pl.allow_split) {
         hipError_t em = fa::launch_merge(a, p->dtype, p->headdim, stream);
         if (em != hipSuccess) return fail(FA_EHIP, "merge launch failed: %s", hipGetErrorString(em));
     }

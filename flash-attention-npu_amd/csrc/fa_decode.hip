@@ -523,8 +523,10 @@ static void launch_decode_t(const FwdArgs& a, int grid, hipStream_t stream) {
 hipError_t launch_decode(const FwdArgs& a, int dtype, int grid, hipStream_t stream) {
     if (dtype == DT_BF16) launch_decode_t<DT_BF16>(a, grid, stream);
     else launch_decode_t<DT_FP16>(a, grid, stream);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_merge(const FwdArgs& a, int dtype, int grid, hipStream_t stream) {
     const int segs = a.B * a.Hk;
     if (dtype == DT_BF16)
         hipLaunchKernelGGL(fa_decode_merge_kernel<DT_BF16>, dim3(segs), dim3(256), 0, stream, a, grid * dec::NWAVE);
