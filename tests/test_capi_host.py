@@ -1,0 +1,148 @@
+"""Host-side checks of the C ABI (include/fa_mi355x.h) and the torch operator
+layer, with no GPU: the library loads and exports every declared entry point,
+the ctypes mirror of fa_fwd_params has the C layout, fa_validate rejects bad
+arguments with the reference's messages, the operators have meta shapes, and
+nothing falls back to a CPU path."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+import torch
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "fa_mi355x.h")
+PKG = os.path.join(REPO, "flash-attention-npu_amd")
+
+
+@pytest.fixture(scope="module")
+def capi():
+    lib = os.path.join(PKG, "fa_mi355x", "lib", "libfa_mi355x.so")
+    if not os.path.exists(lib):
+        subprocess.run([sys.executable, os.path.join(PKG, "build.py")], check=True)
+    from fa_mi355x import capi as c
+    return c
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(fa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol(capi):
+    names = header_functions()
+    assert len(names) >= 8, names
+    lib = ctypes.CDLL(capi.CORE_LIB)
+    for n in names:
+        assert hasattr(lib, n), f"libfa_mi355x.so does not export {n}"
+    assert sorted(capi.EXPORTED) == names
+    assert capi.lib().fa_abi_version() == capi.ABI_VERSION == 1
+
+
+def test_params_layout_matches_header(capi, tmp_path):
+    """Compile a probe against the header and compare sizeof/offsetof of every
+    field with the ctypes mirror."""
+    fields = [n for n, _ in capi.FwdParams._fields_]
+    src = tmp_path / "probe.c"
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "fa_mi355x.h"', "int main(void) {",
+             '  printf("size %zu\\n", sizeof(fa_fwd_params));']
+    for n in fields:
+        lines.append(f'  printf("{n} %zu\\n", offsetof(fa_fwd_params, {n}));')
+    lines.append("  return 0; }")
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)], check=True)
+    out = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True, check=True)
+               .stdout.splitlines())
+    assert int(out["size"]) == ctypes.sizeof(capi.FwdParams)
+    for n in fields:
+        assert int(out[n]) == getattr(capi.FwdParams, n).offset, n
+
+
+def _valid(capi, **kw):
+    """A kvcache decode description with fake (aligned, never dereferenced) pointers."""
+    base = dict(dtype=capi.FA_DTYPE_BF16, batch=2, seqlen_q=1, nheads=8, nheads_k=2, headdim=128, headdim_v=128,
+                seqlen_k=256, batch_cache=2, q=0x10000, q_batch_stride=1024, q_row_stride=1024, q_head_stride=128,
+                k=0x20000, k_batch_stride=256 * 256, k_row_stride=256, k_head_stride=128,
+                v=0x30000, v_batch_stride=256 * 256, v_row_stride=256, v_head_stride=128,
+                out=0x40000, out_batch_stride=1024, out_row_stride=1024, out_head_stride=128,
+                softmax_lse=ctypes.cast(0x50000, ctypes.c_void_p), cache_seqlens=0x60000, softmax_scale=0.088,
+                is_causal=1)
+    base.update(kw)
+    return capi.new_params(**base)
+
+
+def test_validate_accepts_a_valid_call(capi):
+    assert capi.validate(_valid(capi), capi.FA_KIND_KVCACHE) == capi.FA_OK
+    assert capi.validate(_valid(capi, k_new=0x70000, v_new=0x80000, seqlen_new=1, knew_batch_stride=256,
+                                knew_row_stride=256, knew_head_stride=128, vnew_batch_stride=256,
+                                vnew_row_stride=256, vnew_head_stride=128), capi.FA_KIND_KVCACHE) == capi.FA_OK
+
+
+BAD = [
+    # (field overrides, kind, expected status, message fragment)
+    (dict(abi_version=7), 0, "EINVAL", "abi_version"),
+    (dict(dtype=2), 0, "EINVAL", "only support fp16 and bf16"),
+    (dict(nheads=6, nheads_k=4), 0, "EINVAL", "must divide number of heads in query"),
+    (dict(headdim=64, headdim_v=64), 0, "EUNSUPPORTED", "headdim 64"),
+    (dict(dropout_p=0.1), 1, "EUNSUPPORTED", "dropout"),
+    (dict(q=0x10008), 0, "EINVAL", "16-byte aligned"),
+    (dict(k_row_stride=250), 0, "EINVAL", "k strides"),
+    (dict(k_new=0x70000, seqlen_new=1), 0, "EINVAL", "value must also be passed in"),
+    (dict(rotary_cos=0x90000, rotary_sin=0xA0000, rotary_dim=64, seqlen_ro=16), 0, "EINVAL",
+     "new key / value to be appended"),
+    (dict(batch=0), 0, "EINVAL", "batch size"),
+    (dict(batch=4096), 0, "EINVAL", "exceeds"),
+    (dict(softcap=-1.0), 0, "EINVAL", "softcap"),
+    (dict(batch_cache=1), 0, "EINVAL", "smaller than q batch"),
+    (dict(block_table=0xB0000, page_block_size=0, max_blocks_per_seq=1, block_table_rows=2), 0, "EINVAL",
+     "page_block_size"),
+    (dict(alibi_slopes=ctypes.cast(0xC0000, ctypes.c_void_p), alibi_batch_stride=3), 0, "EINVAL", "alibi_slopes"),
+    (dict(), 2, "EINVAL", "cu_seqlens_q is required"),
+    (dict(block_table=0xB0000, page_block_size=16, max_blocks_per_seq=1), 1, "EINVAL", "dense forward"),
+]
+
+
+@pytest.mark.parametrize("over,kind,status,frag", BAD, ids=[b[3] for b in BAD])
+def test_validate_rejects(capi, over, kind, status, frag):
+    p = _valid(capi, **over)
+    st = capi.validate(p, kind)
+    assert st == getattr(capi, "FA_" + status), (st, capi.last_error())
+    assert frag in capi.last_error()
+
+
+def test_operators_have_meta_shapes():
+    import fa_mi355x
+    ops = fa_mi355x.ops
+    m = "meta"
+    q = torch.empty(2, 3, 8, 128, dtype=torch.bfloat16, device=m)
+    kc = torch.empty(2, 64, 2, 128, dtype=torch.bfloat16, device=m)
+    o, l = ops.fwd_kvcache(q, kc, kc, None, None, None, None, None, None, None, None, None, 0.1, True, -1, 0, 0.0,
+                           True, 0)
+    assert o.shape == q.shape and l.shape == (2, 8, 3) and l.dtype == torch.float32
+    o, l = ops.fwd(q, kc, kc, None, 0.0, 0.1, True, -1, 0, 0.0)
+    assert o.shape == q.shape and l.shape == (2, 8, 3)
+    qv = torch.empty(10, 8, 128, dtype=torch.float16, device=m)
+    kv = torch.empty(20, 2, 128, dtype=torch.float16, device=m)
+    cu = torch.empty(3, dtype=torch.int32, device=m)
+    o, l = ops.varlen_fwd(qv, kv, kv, cu, cu, None, None, None, 5, 10, 0.0, 0.1, True, -1, 0, 0.0)
+    assert o.shape == qv.shape and l.shape == (8, 10)
+    op = torch.empty(4, 2, 3, 8, 128, dtype=torch.float32, device=m)
+    lp = torch.empty(4, 2, 3, 8, dtype=torch.float32, device=m)
+    o, l = ops.fwd_combine(op, lp, None, torch.bfloat16)
+    assert o.shape == (2, 3, 8, 128) and o.dtype == torch.bfloat16 and l.shape == (2, 3, 8)
+
+
+def test_no_cpu_fallback():
+    """The public APIs run only the HIP kernels: CPU tensors raise instead of
+    silently computing somewhere else."""
+    import flash_attn_npu_v2
+    q = torch.randn(1, 1, 4, 128, dtype=torch.bfloat16)
+    kc = torch.randn(1, 16, 1, 128, dtype=torch.bfloat16)
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        flash_attn_npu_v2.flash_attn_with_kvcache(q, kc, kc, cache_seqlens=4, causal=True)
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        flash_attn_npu_v2.flash_attn_func(q, kc, kc, causal=True)
