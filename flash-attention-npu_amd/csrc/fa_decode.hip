@@ -404,10 +404,11 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         }
     };
 
-    // prologue: issue the first STAGES-1 tiles, then the first segment's q
+    // prologue: the first segment's q, then the first STAGES-1 tiles (loads
+    // return in order, so q issued first is not held behind the K/V tiles)
+    begin_seg(cs);
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st) issue(t0 + st, kr[st], vr[st], bk[st]);
-    begin_seg(cs);
 
     for (int tb = t0; tb < t1; tb += STAGES) {
 #pragma unroll
@@ -428,60 +429,109 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     end_seg(cs);
 }
 
-// Merges the partials of segments cut by worker boundaries; writes out = 0,
-// lse = +inf for segments with no visible key. One workgroup per segment.
+// Merge of the partials a segment left in the decode kernel (one workgroup
+// per segment; a segment with no visible key gets out = 0, lse = +inf): per
+// row, lse = M + ln(sum_j exp(lse_j - M)) and O = sum_j exp(lse_j - lse) * O_j
+// (the closed form of CombineScale.hpp:150-194). The partial list of a
+// segment [S, S+n) is known from the worker split alone: workers
+// owner(S)..owner(S+n-1) when every worker has a tile (T >= W), else one
+// worker per tile. Phase 1 reduces max / sum of the partial LSEs over
+// threads; phase 2 spreads the independent partial-O loads over NG groups of
+// threads and reduces the groups in LDS, so no load waits on another.
 template <int DT>
 __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int workers) {
     using namespace dec;
+    __shared__ float s_m[16][17], s_s[16][17];
+    __shared__ __attribute__((aligned(16))) float s_acc[256][8];
     const int sig = blockIdx.x;
     const int b = sig / a.Hk, hk = sig % a.Hk;
     if (b >= a.B) return;
     int sq = a.cu_seqlens_q ? a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b] : a.Sq;
     sq = min(max(sq, 0), a.Sq);
     const int rows = sq * a.g;
-    const int rr = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
-    if (rr >= rows) return;
+    if (rows <= 0) return;
     const long long T = a.sched[a.B];
     const int per = (a.sched[b + 1] - a.sched[b]) / a.Hk;
     const long long S = a.sched[b] + (long long)hk * per;
     const long long W = workers;
-    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    float lse = INFINITY;
+    const int tid = threadIdx.x;
+    auto owner = [&](long long t) { return ((t + 1) * W - 1) / T; };
+    long long wf = 0;
+    int n = 0;
     if (per > 0) {
-        // owner(t) = the worker whose range [w*T/W, (w+1)*T/W) holds tile t;
-        // workers with empty ranges (T < W) own nothing and are skipped by
-        // hopping to owner(end of range). One pass with a running maximum.
-        auto owner = [&](long long t) { return ((t + 1) * W - 1) / T; };
-        const long long E = S + per;
-        const long long wf = owner(S), wl = owner(E - 1);
-        if (wf == wl) return;  // one worker owned it and wrote the result
+        wf = owner(S);
+        n = T >= W ? (int)(owner(S + per - 1) - wf + 1) : per;
+        if (n == 1) return;  // one worker owned the segment and wrote the result
+    }
+    // partial j of this segment -> its first partial row
+    auto prow0 = [&](int j) -> long long {
+        const long long w = T >= W ? wf + j : owner(S + j);
+        const int slot = (j == 0 && w * T / W < S) ? 1 : 0;
+        return (w * 2 + slot) * 16;
+    };
+    // ---- phase 1: per-row max and sum over the partial LSEs -----------------------
+    {
+        const int rr = tid & 15, js = tid >> 4;
         float m = -INFINITY, sum = 0.f;
-        long long w = wf;
-        int slot = (wf * T / W) < S ? 1 : 0;
-        while (true) {
-            const long long prow = (w * 2 + slot) * 16 + rr;
-            const float v = a.part_lse[prow];
+        if (rr < rows) {
+            for (int j = js; j < n; j += 16) {
+                const float v = a.part_lse[prow0(j) + rr];
+                if (v != -INFINITY) {
+                    const float mn = fmaxf(m, v);
+                    sum = sum * fast_exp2((m - mn) * kLog2e) + fast_exp2((v - mn) * kLog2e);
+                    m = mn;
+                }
+            }
+        }
+        s_m[rr][js] = m;
+        s_s[rr][js] = sum;
+    }
+    __syncthreads();
+    if (tid < 16) {
+        float m = -INFINITY, sum = 0.f;
+        for (int k = 0; k < 16; ++k) {
+            const float v = s_m[tid][k];
             if (v != -INFINITY) {
-                const f32x4 o0 = *reinterpret_cast<const f32x4*>(a.part_o + prow * D + d0);
-                const f32x4 o1 = *reinterpret_cast<const f32x4*>(a.part_o + prow * D + d0 + 4);
                 const float mn = fmaxf(m, v);
-                const float sc = fast_exp2((m - mn) * kLog2e), wgt = fast_exp2((v - mn) * kLog2e);
-                acc0 = acc0 * sc + o0 * wgt;
-                acc1 = acc1 * sc + o1 * wgt;
-                sum = sum * sc + wgt;
+                sum = sum * fast_exp2((m - mn) * kLog2e) + s_s[tid][k] * fast_exp2((v - mn) * kLog2e);
                 m = mn;
             }
-            slot = 0;
-            if (w == wl) break;
-            w = (T >= W) ? w + 1 : owner((w + 1) * T / W);
         }
-        if (m != -INFINITY) {
-            const float inv = 1.f / sum;
-            acc0 *= inv;
-            acc1 *= inv;
-            lse = m + fast_log2(sum) * kLn2;
+        // lse of the row; -inf marks a row with no visible key
+        s_m[tid][16] = m == -INFINITY ? -INFINITY : m + fast_log2(sum) * kLn2;
+    }
+    __syncthreads();
+    // ---- phase 2: O = sum_j exp(lse_j - lse) O_j over NG groups of threads ----------
+    int rp = 1;
+    while (rp < rows) rp <<= 1;
+    const int NG = 256 / (16 * rp);
+    const int grp = tid / (16 * rp), rem = tid % (16 * rp);
+    const int rr = rem >> 4, d0 = (rem & 15) * 8;
+    const float L = rr < rows ? s_m[rr][16] : -INFINITY;
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    if (rr < rows && L != -INFINITY) {
+#pragma unroll 4
+        for (int j = grp; j < n; j += NG) {
+            const long long pr = prow0(j) + rr;
+            const float v = a.part_lse[pr];
+            const f32x4 o0 = *reinterpret_cast<const f32x4*>(a.part_o + pr * D + d0);
+            const f32x4 o1 = *reinterpret_cast<const f32x4*>(a.part_o + pr * D + d0 + 4);
+            const float wgt = fast_exp2((v - L) * kLog2e);  // exp2(-inf) = 0 for an empty partial
+            acc0 += o0 * wgt;
+            acc1 += o1 * wgt;
         }
     }
+    if (NG > 1) {
+        *reinterpret_cast<f32x4*>(&s_acc[tid][0]) = acc0;
+        *reinterpret_cast<f32x4*>(&s_acc[tid][4]) = acc1;
+        __syncthreads();
+        if (grp != 0) return;
+        for (int gq = 1; gq < NG; ++gq) {
+            acc0 += *reinterpret_cast<const f32x4*>(&s_acc[tid + gq * 16 * rp][0]);
+            acc1 += *reinterpret_cast<const f32x4*>(&s_acc[tid + gq * 16 * rp][4]);
+        }
+    }
+    if (rr >= rows) return;
     const int i = rr / a.g, h = hk * a.g + rr % a.g;
     uint16_t* op = static_cast<uint16_t*>(a.out);
     uint16_t* orow = a.cu_seqlens_q ? op + ((int64_t)a.cu_seqlens_q[b] + i) * a.o_si + (int64_t)h * a.o_sh
@@ -492,7 +542,7 @@ __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int wor
     if (d0 == 0) {
         const int64_t off = a.cu_seqlens_q ? (int64_t)h * a.lse_sh + a.cu_seqlens_q[b] + i
                                            : (int64_t)b * a.lse_sb + (int64_t)h * a.lse_sh + i;
-        a.lse[off] = lse;
+        a.lse[off] = L == -INFINITY ? INFINITY : L;
     }
 }
 

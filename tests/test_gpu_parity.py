@@ -185,12 +185,43 @@ def test_v3_kvcache_paged():
                 api="v3")
 
 
-# ---- split-KV merge: repeated calls reuse the self-clearing arrival counters -----------------
-def test_split_counters_reset_across_calls():
+# ---- split-KV merge: repeated calls reuse the workspace ------------------------------------------
+def test_split_repeated_calls():
     print("case repeated split calls", flush=True)
     for rep in range(3):
         run_kvcache(5, 1, 32, 8, 128, torch.bfloat16, 4096, [4000, 100, 2500, 3000, 1], s_new=1, causal=True,
                     num_splits=0, seed=20)
+
+
+# ---- decode at scale: thousands of 32-key tiles, segments cut by many wave workers ------------
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_large_contiguous(dtype):
+    print(f"case large decode contiguous {dtype}", flush=True)
+    rng = np.random.default_rng(31)
+    seqlens = rng.integers(1024, 8191, size=16)
+    for rep in range(2):
+        run_kvcache(16, 1, 32, 8, 128, dtype, 8192, seqlens, s_new=1, causal=True, seed=31 + rep)
+
+
+def test_decode_large_paged_uneven():
+    print("case large decode paged uneven", flush=True)
+    rng = np.random.default_rng(32)
+    seqlens = np.round(np.exp(rng.uniform(np.log(512), np.log(32768), size=12))).astype(np.int64)
+    run_kvcache(12, 1, 64, 8, 128, torch.bfloat16, 0, seqlens, s_new=1, page=256, causal=True, seed=32)
+
+
+def test_decode_one_long_sequence():
+    # one (sequence, kv head) segment spans every wave worker: the merge combines ~1024 partials
+    print("case decode one long sequence", flush=True)
+    run_kvcache(1, 1, 8, 1, 128, torch.bfloat16, 140000, [139000], s_new=1, causal=True, seed=33)
+
+
+def test_decode_large_verify_window_alibi():
+    print("case large spec-verify window alibi", flush=True)
+    rng = np.random.default_rng(34)
+    seqlens = rng.integers(16384, 65536, size=8)
+    run_kvcache(8, 4, 32, 8, 128, torch.bfloat16, 0, seqlens, s_new=0, page=256, causal=True, window=(4096, 0),
+                alibi=True, batch_idx=True, seed=34)
 
 
 def test_prefill_shape_split_small_batch():
