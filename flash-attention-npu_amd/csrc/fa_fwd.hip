@@ -368,6 +368,17 @@ __global__ void __launch_bounds__(pf::NT, 1) fa_prefill_kernel(FwdArgs a) {
                     for (int rb = 0; rb < RB; ++rb) sacc[rb][kb] = mfma16x16x32<DT>(av, qreg[rb][s], sacc[rb][kb]);
                 }
             }
+            // V^T operands for this half tile (transpose reads), issued now so
+            // the LDS latency hides under the softmax below
+            u32x4 vt[DBLK];
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db) {
+                const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_v[buf][offv[db] + (32 * hh) * D]);
+                const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_v[buf][offv[db] + (32 * hh + 16) * D]);
+                const u32x2 l2 = __builtin_bit_cast(u32x2, lo4);
+                const u32x2 h2 = __builtin_bit_cast(u32x2, hi4);
+                vt[db] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+            }
             // scores (log2 units when BIAS; raw otherwise, scaled inside exp2's FMA)
             float xmax[RB];
             bool need = false;
@@ -434,17 +445,11 @@ __global__ void __launch_bounds__(pf::NT, 1) fa_prefill_kernel(FwdArgs a) {
                 f32x8 v8 = {p[0][0], p[0][1], p[0][2], p[0][3], p[1][0], p[1][1], p[1][2], p[1][3]};
                 pk[rb] = pack8<DT>(v8);
             }
-            // O^T += V^T . P^T (V^T from transpose reads)
+            // O^T += V^T . P^T
 #pragma unroll
-            for (int db = 0; db < DBLK; ++db) {
-                const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_v[buf][offv[db] + (32 * hh) * D]);
-                const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_v[buf][offv[db] + (32 * hh + 16) * D]);
-                const u32x2 l2 = __builtin_bit_cast(u32x2, lo4);
-                const u32x2 h2 = __builtin_bit_cast(u32x2, hi4);
-                const u32x4 av = {l2[0], l2[1], h2[0], h2[1]};
+            for (int db = 0; db < DBLK; ++db)
 #pragma unroll
-                for (int rb = 0; rb < RB; ++rb) oacc[rb][db] = mfma16x16x32<DT>(av, pk[rb], oacc[rb][db]);
-            }
+                for (int rb = 0; rb < RB; ++rb) oacc[rb][db] = mfma16x16x32<DT>(vt[db], pk[rb], oacc[rb][db]);
         };
 
         if (ntiles > 0) {
