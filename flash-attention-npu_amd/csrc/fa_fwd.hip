@@ -291,6 +291,11 @@ __global__ void __launch_bounds__(pf::NT, 1) fa_prefill_kernel(FwdArgs a) {
                 qreg[rb][s] = ok ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s) * 8) : u32x4{0u, 0u, 0u, 0u};
         }
 
+        // Retire the q loads here. Otherwise the wait-count tracking merges
+        // them with the K/V prefetch at the tile loop's back edge and waits
+        // for that prefetch (vmcnt(0)) before every QK product.
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt, lgkmcnt unconstrained
+
         f32x4 oacc[RB][DBLK];
         float m_run[RB], l_run[RB];
 #pragma unroll
