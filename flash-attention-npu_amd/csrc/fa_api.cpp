@@ -104,8 +104,10 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
     FA_CHECK(p->nheads >= 1 && p->nheads_k >= 1, "number of heads must be positive");
     FA_CHECK(p->nheads % p->nheads_k == 0, "Number of heads in key/value must divide number of heads in query");
     FA_CHECK(p->headdim >= 1, "head dimension must be positive");
-    if (p->headdim != 128)
-        return fail(FA_EUNSUPPORTED, "headdim %d is not supported by this build (supported: 128)", p->headdim);
+    FA_CHECK(p->headdim % 8 == 0, "head dimension must be a multiple of 8");
+    if (p->headdim > 128)
+        return fail(FA_EUNSUPPORTED, "headdim %d is not supported by this build (supported: multiples of 8 up to 128)",
+                    p->headdim);
     FA_CHECK(p->headdim_v == p->headdim, "headdim_v (%d) must equal headdim (%d)", p->headdim_v, p->headdim);
     if (p->dropout_p != 0.f) return fail(FA_EUNSUPPORTED, "dropout is not supported (forward inference only)");
     FA_CHECK(p->softcap >= 0.f, "softcap must be >= 0");
@@ -355,6 +357,7 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
     a.H = p->nheads;
     a.Hk = p->nheads_k;
     a.g = pl.g;
+    a.hd = p->headdim;
     a.seqlen_new = (kind == FA_KIND_KVCACHE && p->k_new) ? p->seqlen_new : 0;
     if (fused_append) {
         a.k_new = p->k_new;
@@ -395,14 +398,14 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
 
     mark(1);
     hipError_t e = pl.decode ? fa::launch_decode(a, p->dtype, pl.grid, stream)
-                             : fa::launch_fwd(a, p->dtype, p->headdim, pl.grid, stream);
+                             : fa::launch_fwd(a, p->dtype, 128, pl.grid, stream);
     if (e != hipSuccess) return fail(FA_EHIP, "attention launch failed: %s", hipGetErrorString(e));
     mark(2);
     if (pl.decode) {
         hipError_t em = fa::launch_decode_merge(a, p->dtype, pl.grid, stream);
         if (em != hipSuccess) return fail(FA_EHIP, "merge launch failed: %s", hipGetErrorString(em));
     } else if (pl.allow_split) {
-        hipError_t em = fa::launch_merge(a, p->dtype, p->headdim, stream);
+        hipError_t em = fa::launch_merge(a, p->dtype, 128, stream);
         if (em != hipSuccess) return fail(FA_EHIP, "merge launch failed: %s", hipGetErrorString(em));
     }
     mark(3);

@@ -86,8 +86,9 @@ __device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref
 }
 
 // BIAS: softcap or ALiBi present; FUSE: append k_new/v_new in this kernel;
-// LAYOUT: 0 = batch-strided cache, 1 = paged with page % 32 == 0, 2 = any.
-template <int DT, int STAGES, bool BIAS, bool FUSE, int LAYOUT>
+// LAYOUT: 0 = batch-strided cache, 1 = paged with page % 32 == 0, 2 = any;
+// HDM: head dim below 128 (dims >= a.hd read as zero, never written).
+template <int DT, int STAGES, bool BIAS, bool FUSE, int LAYOUT, bool HDM = false>
 __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     using namespace dec;
     __shared__ int s_pref[MAXB + 1];
@@ -217,8 +218,9 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                 }
 #pragma unroll
                 for (int s = 0; s < KSTEPS; ++s) {
-                    kk[h][s] = *reinterpret_cast<const u32x4*>(kpr + s * 8);
-                    vv[h][s] = *reinterpret_cast<const u32x4*>(vpr + s * 8);
+                    const bool in = !HDM || G * 32 + s * 8 < a.hd;
+                    kk[h][s] = in ? *reinterpret_cast<const u32x4*>(kpr + s * 8) : u32x4{0u, 0u, 0u, 0u};
+                    vv[h][s] = in ? *reinterpret_cast<const u32x4*>(vpr + s * 8) : u32x4{0u, 0u, 0u, 0u};
                 }
             } else {
 #pragma unroll
@@ -251,7 +253,8 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                                    : qp + (int64_t)s.b * a.q_sb + (int64_t)i * a.q_si + (int64_t)h * a.q_sh;
 #pragma unroll
         for (int s2 = 0; s2 < KSTEPS; ++s2)
-            qreg[s2] = ok ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s2) * 8) : u32x4{0u, 0u, 0u, 0u};
+            qreg[s2] = ok && (!HDM || (G * KSTEPS + s2) * 8 < a.hd) ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s2) * 8)
+                                                          : u32x4{0u, 0u, 0u, 0u};
         m_run = -INFINITY;
         l_run = 0.f;
 #pragma unroll
@@ -272,6 +275,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                                  : op + (int64_t)s.b * a.o_sb + (int64_t)i * a.o_si + (int64_t)h * a.o_sh;
 #pragma unroll
             for (int db = 0; db < DBLK; ++db) {
+                if (HDM && 16 * db + 4 * G >= a.hd) continue;
                 f32x4 o = oacc[db] * inv;
                 uint16_t h4[4] = {f32_to_16<DT>(o[0]), f32_to_16<DT>(o[1]), f32_to_16<DT>(o[2]), f32_to_16<DT>(o[3])};
                 *reinterpret_cast<u32x2*>(orow + 16 * db + 4 * G) = __builtin_bit_cast(u32x2, h4);
@@ -306,8 +310,10 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                     uint16_t* vd = const_cast<uint16_t*>(row_ptr(vc, a.v_sb, a.v_si, a.v_sh, cs, key, blk)) + G * 32;
 #pragma unroll
                     for (int s = 0; s < KSTEPS; ++s) {
-                        *reinterpret_cast<u32x4*>(kd + s * 8) = kk[h][s];
-                        *reinterpret_cast<u32x4*>(vd + s * 8) = vv[h][s];
+                        if (!HDM || G * 32 + s * 8 < a.hd) {
+                            *reinterpret_cast<u32x4*>(kd + s * 8) = kk[h][s];
+                            *reinterpret_cast<u32x4*>(vd + s * 8) = vv[h][s];
+                        }
                     }
                 }
             }
@@ -538,7 +544,7 @@ __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int wor
                                     : op + (int64_t)b * a.o_sb + (int64_t)i * a.o_si + (int64_t)h * a.o_sh;
     uint16_t h8[8] = {f32_to_16<DT>(acc0[0]), f32_to_16<DT>(acc0[1]), f32_to_16<DT>(acc0[2]), f32_to_16<DT>(acc0[3]),
                       f32_to_16<DT>(acc1[0]), f32_to_16<DT>(acc1[1]), f32_to_16<DT>(acc1[2]), f32_to_16<DT>(acc1[3])};
-    *reinterpret_cast<u32x4*>(orow + d0) = __builtin_bit_cast(u32x4, h8);
+    if (d0 < a.hd) *reinterpret_cast<u32x4*>(orow + d0) = __builtin_bit_cast(u32x4, h8);
     if (d0 == 0) {
         const int64_t off = a.cu_seqlens_q ? (int64_t)h * a.lse_sh + a.cu_seqlens_q[b] + i
                                            : (int64_t)b * a.lse_sb + (int64_t)h * a.lse_sh + i;
@@ -565,6 +571,13 @@ static void launch_decode_l(const FwdArgs& a, int grid, hipStream_t stream) {
 
 template <int DT>
 static void launch_decode_t(const FwdArgs& a, int grid, hipStream_t stream) {
+    if (a.hd < dec::D) {
+        // head dims below 128: the generic-layout, bias-capable instances
+        // with dim masking (correct for every input of this kernel)
+        if (a.k_new) hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, true, true, 2, true>), dim3(grid), dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, true, false, 2, true>), dim3(grid), dim3(256), 0, stream, a);
+        return;
+    }
     if (a.block_table && (a.page % dec::KT) == 0) launch_decode_l<DT, 1>(a, grid, stream);
     else if (a.block_table || a.cu_seqlens_k) launch_decode_l<DT, 2>(a, grid, stream);
     else launch_decode_l<DT, 0>(a, grid, stream);

@@ -288,7 +288,8 @@ __global__ void __launch_bounds__(pf::NT, 1) fa_prefill_kernel(FwdArgs a) {
                                        : qp + (int64_t)b * a.q_sb + (int64_t)i * a.q_si + (int64_t)h * a.q_sh;
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s)
-                qreg[rb][s] = ok ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s) * 8) : u32x4{0u, 0u, 0u, 0u};
+                qreg[rb][s] = ok && (G * KSTEPS + s) * 8 < a.hd ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s) * 8)
+                                                                : u32x4{0u, 0u, 0u, 0u};
         }
 
         // Retire the q loads here. Otherwise the wait-count tracking merges
@@ -325,7 +326,7 @@ __global__ void __launch_bounds__(pf::NT, 1) fa_prefill_kernel(FwdArgs a) {
 #pragma unroll
             for (int u = 0; u < CPT; ++u) {
                 const int j = t0 + kk0 + u * (NT / DCH);
-                if (j < k_hi) {
+                if (j < k_hi && dch * 8 < a.hd) {
                     const uint16_t* kpr;
                     const uint16_t* vpr;
                     if constexpr (PAGED) {
@@ -506,6 +507,7 @@ __global__ void __launch_bounds__(pf::NT, 1) fa_prefill_kernel(FwdArgs a) {
                                          : op + (int64_t)b * a.o_sb + (int64_t)i * a.o_si + (int64_t)h * a.o_sh;
 #pragma unroll
                     for (int db = 0; db < DBLK; ++db) {
+                        if (16 * db + 4 * G >= a.hd) continue;
                         const f32x4 o = oacc[rb][db] * inv;
                         uint16_t h4[4] = {f32_to_16<DT>(o[0]), f32_to_16<DT>(o[1]), f32_to_16<DT>(o[2]), f32_to_16<DT>(o[3])};
                         *reinterpret_cast<u32x2*>(orow + 16 * db + 4 * G) = __builtin_bit_cast(u32x2, h4);
@@ -580,7 +582,7 @@ __global__ void __launch_bounds__(256) fa_merge_kernel(FwdArgs a) {
     else orow = op + (int64_t)b * a.o_sb + (int64_t)i * a.o_si + (int64_t)h * a.o_sh;
     uint16_t h8[8] = {f32_to_16<DT>(acc0[0]), f32_to_16<DT>(acc0[1]), f32_to_16<DT>(acc0[2]), f32_to_16<DT>(acc0[3]),
                       f32_to_16<DT>(acc1[0]), f32_to_16<DT>(acc1[1]), f32_to_16<DT>(acc1[2]), f32_to_16<DT>(acc1[3])};
-    *reinterpret_cast<u32x4*>(orow + d0) = __builtin_bit_cast(u32x4, h8);
+    if (d0 < a.hd) *reinterpret_cast<u32x4*>(orow + d0) = __builtin_bit_cast(u32x4, h8);
     if (d0 == 0) {
         int64_t lo_off = a.cu_seqlens_q ? (int64_t)h * a.lse_sh + a.cu_seqlens_q[b] + i
                                         : (int64_t)b * a.lse_sb + (int64_t)h * a.lse_sh + i;

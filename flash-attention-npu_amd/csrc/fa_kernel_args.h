@@ -37,6 +37,8 @@ struct FwdArgs {
     float softcap;      // 0 = off
 
     int B, Sq, Sk, H, Hk, g;
+    int hd;             // head dim present in memory (multiple of 8, <= the kernel's 128;
+                        // the dims above it are read as zeros and never written)
     int seqlen_new;     // tokens appended this call (added to seqlens_k)
     int wl, wr;         // normalised window, -1 = unbounded, causal => wr = 0
     int page;           // paged: tokens per block

@@ -185,6 +185,52 @@ def test_v3_kvcache_paged():
                 api="v3")
 
 
+# ---- head dims below 128 (dims above D are zero inside the kernels, never written) -----------
+@pytest.mark.parametrize("D", [64, 80, 96])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_headdim_dense(D, dtype):
+    print(f"case headdim dense D={D} {dtype}", flush=True)
+    run_dense(2, 150, 260, 8, 2, D, dtype, causal=True, seed=40 + D)
+
+
+@pytest.mark.parametrize("D", [64, 96])
+def test_headdim_decode_paged_append(D):
+    print(f"case headdim decode paged D={D}", flush=True)
+    run_kvcache(5, 1, 32, 8, D, torch.bfloat16, 0, [700, 33, 4000, 1, 2500], s_new=1, page=64, causal=True,
+                seed=50 + D)
+
+
+def test_headdim_decode_contiguous_fused_append_large():
+    print("case headdim decode contiguous D=64 large", flush=True)
+    rng = np.random.default_rng(52)
+    run_kvcache(16, 1, 32, 8, 64, torch.float16, 8192, rng.integers(1024, 8191, size=16), s_new=1, causal=True,
+                seed=52)
+
+
+@pytest.mark.parametrize("rotary", ["neox", "interleaved"])
+def test_headdim_chunked_prefill_rotary(rotary):
+    print(f"case headdim 64 chunked prefill rotary {rotary}", flush=True)
+    run_kvcache(2, 80, 16, 4, 64, torch.bfloat16, 400, [200, 57], s_new=80, rotary=rotary, causal=True, seed=53)
+
+
+def test_headdim_padded_to_multiple_of_8():
+    # the v2 API pads the head dim to a multiple of 8 and slices the output (interface_arch22.py:1102-1176)
+    import flash_attn_npu_v2
+    print("case headdim 36 padded", flush=True)
+    g = _gen(54)
+    q = randn((2, 40, 4, 36), torch.float16, g, "cpu")
+    k = randn((2, 70, 2, 36), torch.float16, g, "cpu")
+    v = randn((2, 70, 2, 36), torch.float16, g, "cpu")
+    ref_out, ref_lse = orc.attention(bits(q).reshape(q.shape), bits(k).reshape(k.shape), bits(v).reshape(v.shape),
+                                     dtype=orc.FP16, scale=36 ** -0.5, causal=True, nthreads=NT)
+    out, lse, _ = flash_attn_npu_v2.flash_attn_func(q.to(DEV), k.to(DEV), v.to(DEV), causal=True,
+                                                    return_attn_probs=True)
+    torch.cuda.synchronize()
+    assert out.shape == q.shape
+    assert_close_out(out, ref_out, torch.float16)
+    assert_close_lse(lse, ref_lse)
+
+
 # ---- split-KV merge: repeated calls reuse the workspace ------------------------------------------
 def test_split_repeated_calls():
     print("case repeated split calls", flush=True)
