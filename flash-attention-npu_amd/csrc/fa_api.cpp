@@ -227,7 +227,8 @@ void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
     pl.off_po = off;
     if (pl.allow_split) off = align256(off + sizeof(float) * (size_t)pl.items_max * pl.BM * p->headdim_v);
     pl.off_qrot = off;
-    if (pl.rotary) off = align256(off + 2 * (size_t)p->batch * p->seqlen_q * p->nheads * p->headdim);
+    // decode reads a rotated copy of q; prefill rotates q as it loads it
+    if (pl.rotary && pl.decode) off = align256(off + 2 * (size_t)p->batch * p->seqlen_q * p->nheads * p->headdim);
     pl.total = off;
 }
 
@@ -256,7 +257,8 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
     };
     mark(0);
     // Decode without rotary appends inside the attention kernel; otherwise the
-    // append (and rotary) runs as its own launch first.
+    // append (with the key rotation, and for decode the q rotation) runs as
+    // its own launch first. Prefill rotates q inside its q load.
     const bool fused_append = kind == FA_KIND_KVCACHE && p->k_new && pl.decode && !pl.rotary;
     if (kind == FA_KIND_KVCACHE && p->k_new && !fused_append) {
         fa::KvPrepArgs k{};
@@ -295,7 +297,7 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
         k.q_sb = p->q_batch_stride;
         k.q_si = p->q_row_stride;
         k.q_sh = p->q_head_stride;
-        k.q_out = pl.rotary ? ws + pl.off_qrot : nullptr;
+        k.q_out = pl.rotary && pl.decode ? ws + pl.off_qrot : nullptr;
         const bool local = p->window_size_left >= 0 || p->window_size_right >= 0;
         k.q_same_pos = !(p->is_causal || local);
         k.B = p->batch;
@@ -307,7 +309,7 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
         k.Dv = p->headdim_v;
         hipError_t e = fa::launch_kv_prep(k, p->dtype, stream);
         if (e != hipSuccess) return fail(FA_EHIP, "kv_prep launch failed: %s", hipGetErrorString(e));
-        if (pl.rotary) {
+        if (pl.rotary && pl.decode) {
             q_ptr = ws + pl.off_qrot;
             q_sh = p->headdim;
             q_si = (int64_t)p->nheads * p->headdim;
@@ -368,6 +370,14 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
         a.vn_sb = p->vnew_batch_stride;
         a.vn_si = p->vnew_row_stride;
         a.vn_sh = p->vnew_head_stride;
+    }
+    if (pl.rotary && !pl.decode) {
+        a.rot_cos = p->rotary_cos;
+        a.rot_sin = p->rotary_sin;
+        a.rot_dim = p->rotary_dim;
+        a.rot_interleaved = p->rotary_interleaved ? 1 : 0;
+        a.rot_same_pos = !(p->is_causal || p->window_size_left >= 0 || p->window_size_right >= 0);
+        a.seqlen_ro = p->seqlen_ro;
     }
     // window normalisation (flash_api.cpp:483-494): the seqlen-dependent rules
     // leave the mask unchanged, causal forces the right edge to the diagonal

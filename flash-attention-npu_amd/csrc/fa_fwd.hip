@@ -16,9 +16,11 @@
 //     query row and 8 keys, which is exactly the packed P^T operand of
 //     O^T = V^T.P^T. The head dimension of Q/K is permuted (lane group G takes
 //     dims G*D/4 .. +D/4) so every lane reads contiguous 16-byte chunks.
-//   * One workgroup = 4 waves x 64 rows; a wave reuses each K/V operand it
-//     reads from LDS for 4 row blocks, which keeps LDS reads at half the LDS
-//     bandwidth when the matrix cores run at full rate.
+//   * One workgroup = 8 waves x 32 rows (two waves per SIMD); a wave reuses
+//     each K/V operand it reads from LDS for its 2 row blocks of 16. The
+//     256-VGPR budget of two waves per SIMD is what bounds the row blocks.
+//   * With kvcache rotary, q is rotated as it is loaded (ROT), so the rotated
+//     copy is never written to or re-read from HBM.
 //   * K/V tiles (64 keys) are double-buffered in LDS with one barrier per
 //     tile; K uses a 16-byte XOR swizzle on the row, V one on the low row bits
 //     so that both the K operand reads and the ds_read_b64_tr_b16 transpose
@@ -34,6 +36,7 @@
 //     the sequence lengths in LDS; there is no host round trip.
 #include "fa_common.h"
 #include "fa_kernel_args.h"
+#include "fa_rope.h"
 
 #include <type_traits>
 
@@ -43,13 +46,15 @@ constexpr int kMaxBatchLds = 2048;
 
 struct BatchInfo {
     int sq, sk, rows, mt, lo, hi;
+    int len0;  // kvcache: cache_seqlens[b] before this call's append, else 0
 };
 
 template <int BM>
 __device__ __forceinline__ void batch_info(const FwdArgs& a, int b, BatchInfo& bi) {
     int sq = a.cu_seqlens_q ? a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b] : a.Sq;
     int sk;
-    if (a.seqlens_k) sk = a.seqlens_k[b] + a.seqlen_new;  // cache_seqlens / seqused_k
+    bi.len0 = a.seqlens_k ? a.seqlens_k[b] : 0;
+    if (a.seqlens_k) sk = bi.len0 + a.seqlen_new;  // cache_seqlens / seqused_k
     else if (a.cu_seqlens_k) sk = a.cu_seqlens_k[b + 1] - a.cu_seqlens_k[b];
     else sk = a.Sk;
     sq = min(max(sq, 0), a.Sq);  // Sq is max_seqlen_q for varlen: bounds the tiles
@@ -191,8 +196,9 @@ __device__ __forceinline__ int swz_k(int r, int c) { return c ^ (r & 15); }
 __device__ __forceinline__ int swz_v(int r, int c) { return c ^ ((r & 3) << 1) ^ (((r >> 2) & 1) << 3); }
 
 // BIAS: softcap, ALiBi or a non-positive scale (scores are formed explicitly);
-// PAGED: K/V rows come through the block table.
-template <int DT, bool BIAS, bool PAGED>
+// PAGED: K/V rows come through the block table; ROT: q is rotated (kvcache
+// rotary) as it is loaded.
+template <int DT, bool BIAS, bool PAGED, bool ROT>
 __global__ void __launch_bounds__(pf::NT, 1) fa_prefill_kernel(FwdArgs a) {
     using namespace pf;
     __shared__ __attribute__((aligned(16))) uint16_t s_k[2][BN * D];
@@ -271,42 +277,6 @@ __global__ void __launch_bounds__(pf::NT, 1) fa_prefill_kernel(FwdArgs a) {
         const int wi_lo = wave_live ? wrow0 / g : 0;
         const int wi_hi = wave_live ? (wrow0 + wrows - 1) / g : 0;
 
-        // ---- Q operands (B of S^T = K.Q^T), dims permuted by lane group --------------------
-        u32x4 qreg[RB][KSTEPS];
-        float slope[RB];
-        int qi[RB];
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            const int r = wrow0 + rb * 16 + li;
-            const bool ok = r < bi.rows;
-            const int i = ok ? r / g : 0;
-            const int h = hk * g + (ok ? r % g : 0);
-            qi[rb] = i;
-            slope[rb] = (BIAS && a.alibi && ok) ? a.alibi[(int64_t)b * a.alibi_sb + h] : 0.f;
-            const uint16_t* qrow = a.cu_seqlens_q
-                                       ? qp + ((int64_t)a.cu_seqlens_q[b] + i) * a.q_si + (int64_t)h * a.q_sh
-                                       : qp + (int64_t)b * a.q_sb + (int64_t)i * a.q_si + (int64_t)h * a.q_sh;
-#pragma unroll
-            for (int s = 0; s < KSTEPS; ++s)
-                qreg[rb][s] = ok && (G * KSTEPS + s) * 8 < a.hd ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s) * 8)
-                                                                : u32x4{0u, 0u, 0u, 0u};
-        }
-
-        // Retire the q loads here. Otherwise the wait-count tracking merges
-        // them with the K/V prefetch at the tile loop's back edge and waits
-        // for that prefetch (vmcnt(0)) before every QK product.
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt, lgkmcnt unconstrained
-
-        f32x4 oacc[RB][DBLK];
-        float m_run[RB], l_run[RB];
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            m_run[rb] = -1e30f;  // finite floor: exp2(x - m) never forms inf - inf
-            l_run[rb] = 0.f;
-#pragma unroll
-            for (int db = 0; db < DBLK; ++db) oacc[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-
         // ---- K/V tiles: registers -> double-buffered LDS ----------------------------------
         u32x4 kr[CPT], vr[CPT];
         // per-item row bases: token j of this kv head lives at base + j * si
@@ -354,6 +324,90 @@ __global__ void __launch_bounds__(pf::NT, 1) fa_prefill_kernel(FwdArgs a) {
                 *reinterpret_cast<u32x4*>(&s_v[buf][offsv + u * (NT / DCH) * D]) = vr[u];
             }
         };
+
+        // ---- Q operands (B of S^T = K.Q^T), dims permuted by lane group --------------------
+        u32x4 qreg[RB][KSTEPS];
+        float slope[RB];
+        int qi[RB];
+        [[maybe_unused]] const uint16_t* qrows[RB];
+        [[maybe_unused]] bool qok[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const int r = wrow0 + rb * 16 + li;
+            const bool ok = r < bi.rows;
+            const int i = ok ? r / g : 0;
+            const int h = hk * g + (ok ? r % g : 0);
+            qi[rb] = i;
+            slope[rb] = (BIAS && a.alibi && ok) ? a.alibi[(int64_t)b * a.alibi_sb + h] : 0.f;
+            const uint16_t* qrow = a.cu_seqlens_q
+                                       ? qp + ((int64_t)a.cu_seqlens_q[b] + i) * a.q_si + (int64_t)h * a.q_sh
+                                       : qp + (int64_t)b * a.q_sb + (int64_t)i * a.q_si + (int64_t)h * a.q_sh;
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s)
+                qreg[rb][s] = ok && (G * KSTEPS + s) * 8 < a.hd ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s) * 8)
+                                                                : u32x4{0u, 0u, 0u, 0u};
+            qrows[rb] = qrow;
+            qok[rb] = ok;
+        }
+        if constexpr (ROT) {
+            // q[b, i] is rotated at cache_seqlens[b] (+ i when causal or local).
+            // The rotary arguments are read from the argument block here (the
+            // empty asm hides that they are loop invariant), so they hold no
+            // scalar registers across the tile loop, where every scalar
+            // register is taken. FwdArgs is the kernel's only argument.
+            auto kseg = __builtin_amdgcn_kernarg_segment_ptr();
+            asm volatile("" : "+s"(kseg));
+            const FwdArgs* rk = (const FwdArgs*)kseg;
+            const int rot_rd = rk->rot_dim;
+            const bool rot_inter = rk->rot_interleaved != 0;
+            const int clast = (rot_rd >> 3) - 1;
+            // Every operand load is issued before any rotation (chunks past
+            // rotary_dim load the last rotated chunk's operands and keep q),
+            // so the q rows cost one memory round trip, and that trip overlaps
+            // the first K/V tile's.
+            auto rotate_q = [&](auto inter_tag) {
+                constexpr bool INTER = decltype(inter_tag)::value;
+                RopeOps rop[RB][KSTEPS];
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) {
+                    int pos = bi.len0 + (rk->rot_same_pos ? 0 : qi[rb]);
+                    pos = min(max(pos, 0), rk->seqlen_ro - 1);
+                    const uint16_t* crow_c = static_cast<const uint16_t*>(rk->rot_cos) + (int64_t)pos * (rot_rd >> 1);
+                    const uint16_t* crow_s = static_cast<const uint16_t*>(rk->rot_sin) + (int64_t)pos * (rot_rd >> 1);
+#pragma unroll
+                    for (int s = 0; s < KSTEPS; ++s)
+                        rop[rb][s] = rope_load(qrows[rb], min(G * KSTEPS + s, clast), rot_rd, INTER, crow_c, crow_s);
+                }
+                // the first K/V tile's loads go out before the rotation, which
+                // then runs under their latency
+                if (ntiles > 0) load_tile(k_lo);
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int s = 0; s < KSTEPS; ++s) {
+                        const int c = G * KSTEPS + s;
+                        const u32x4 rq = rope_apply<DT>(qreg[rb][s], rop[rb][s], c, rot_rd, INTER);
+                        if (qok[rb] && c <= clast) qreg[rb][s] = rq;
+                    }
+            };
+            if (rot_inter) rotate_q(std::true_type{});
+            else rotate_q(std::false_type{});
+        }
+
+        // Retire the q loads here. Otherwise the wait-count tracking merges
+        // them with the K/V prefetch at the tile loop's back edge and waits
+        // for that prefetch (vmcnt(0)) before every QK product.
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt, lgkmcnt unconstrained
+
+        f32x4 oacc[RB][DBLK];
+        float m_run[RB], l_run[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            m_run[rb] = -1e30f;  // finite floor: exp2(x - m) never forms inf - inf
+            l_run[rb] = 0.f;
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db) oacc[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
 
         // 32 keys (half of the LDS tile at key offset 32*hh) for this wave's 64
         // rows; MASK: apply the per-key test
@@ -459,7 +513,7 @@ __global__ void __launch_bounds__(pf::NT, 1) fa_prefill_kernel(FwdArgs a) {
         };
 
         if (ntiles > 0) {
-            load_tile(k_lo);
+            if constexpr (!ROT) load_tile(k_lo);  // ROT issued it with the q rotation
             store_tile(0);
             if (ntiles > 1) load_tile(k_lo + BN);
         }
@@ -636,10 +690,16 @@ __global__ void __launch_bounds__(256) fa_combine_flat_kernel(const float* __res
 int fwd_tile_rows() { return pf::BM; }
 int fwd_tile_keys() { return pf::BN; }
 
+template <int DT, bool BIAS, bool ROT>
+static void launch_prefill_r(const FwdArgs& a, int grid, hipStream_t stream) {
+    if (a.block_table) hipLaunchKernelGGL((fa_prefill_kernel<DT, BIAS, true, ROT>), dim3(grid), dim3(pf::NT), 0, stream, a);
+    else hipLaunchKernelGGL((fa_prefill_kernel<DT, BIAS, false, ROT>), dim3(grid), dim3(pf::NT), 0, stream, a);
+}
+
 template <int DT, bool BIAS>
 static void launch_prefill_b(const FwdArgs& a, int grid, hipStream_t stream) {
-    if (a.block_table) hipLaunchKernelGGL((fa_prefill_kernel<DT, BIAS, true>), dim3(grid), dim3(pf::NT), 0, stream, a);
-    else hipLaunchKernelGGL((fa_prefill_kernel<DT, BIAS, false>), dim3(grid), dim3(pf::NT), 0, stream, a);
+    if (a.rot_cos) launch_prefill_r<DT, BIAS, true>(a, grid, stream);
+    else launch_prefill_r<DT, BIAS, false>(a, grid, stream);
 }
 
 hipError_t launch_fwd(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream) {

@@ -62,6 +62,11 @@ struct FwdArgs {
     int64_t kn_sb, kn_si, kn_sh;
     const void* v_new;
     int64_t vn_sb, vn_si, vn_sh;
+    // prefill with rotary: q is rotated as it is loaded (cos/sin: (seqlen_ro, rot_dim/2));
+    // rot_cos == nullptr means q is used as stored
+    const void* rot_cos;
+    const void* rot_sin;
+    int rot_dim, rot_interleaved, rot_same_pos, seqlen_ro;
 };
 
 struct KvPrepArgs {
@@ -84,7 +89,7 @@ struct KvPrepArgs {
     const void* sin;
     int64_t cs_stride;
     int rotary_dim, interleaved, seqlen_ro;
-    // q rotation: q (B, Sq, H, D) -> q_out (B, Sq, H, D) contiguous
+    // q rotation (decode): q (B, Sq, H, D) -> q_out (B, Sq, H, D) contiguous; null = none
     const void* q;
     int64_t q_sb, q_si, q_sh;
     void* q_out;
