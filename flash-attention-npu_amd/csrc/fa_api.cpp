@@ -22,8 +22,8 @@
 #include "fa_kernel_args.h"
 
 namespace fa {
-int fwd_tile_rows();
-int fwd_tile_keys();
+int fwd_tile_rows(int d);
+int fwd_tile_keys(int d);
 int decode_workers(int cus);
 hipError_t launch_fwd(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream);
 hipError_t launch_merge(const FwdArgs& a, int dtype, int d, hipStream_t stream);
@@ -87,6 +87,7 @@ struct Plan {
     int grid;
     bool rotary;
     int workers;        // decode: wave workers
+    int kd;             // kernel head dim (128 or 256)
     size_t off_sched, off_plse, off_po, off_qrot, total;
 };
 
@@ -105,9 +106,7 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
     FA_CHECK(p->nheads % p->nheads_k == 0, "Number of heads in key/value must divide number of heads in query");
     FA_CHECK(p->headdim >= 1, "head dimension must be positive");
     FA_CHECK(p->headdim % 8 == 0, "head dimension must be a multiple of 8");
-    if (p->headdim > 128)
-        return fail(FA_EUNSUPPORTED, "headdim %d is not supported by this build (supported: multiples of 8 up to 128)",
-                    p->headdim);
+    FA_CHECK(p->headdim <= 256, "FlashAttention only supports head dimension at most 256");
     FA_CHECK(p->headdim_v == p->headdim, "headdim_v (%d) must equal headdim (%d)", p->headdim_v, p->headdim);
     if (p->dropout_p != 0.f) return fail(FA_EUNSUPPORTED, "dropout is not supported (forward inference only)");
     FA_CHECK(p->softcap >= 0.f, "softcap must be >= 0");
@@ -179,9 +178,13 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
 void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
     pl.g = p->nheads / p->nheads_k;
     pl.rows_max = p->seqlen_q * pl.g;
-    pl.decode = pl.rows_max <= kDecodeRows;
-    pl.BM = pl.decode ? kDecodeRows : fa::fwd_tile_rows();
-    pl.BN = pl.decode ? 32 : fa::fwd_tile_keys();
+    // kernel head dim: the 128 kernels serve head dims up to 128 (the dims
+    // above the real ones read as zero), the 256 prefill kernel the rest;
+    // decode shapes above 128 run on the prefill kernel
+    pl.kd = p->headdim <= 128 ? 128 : 256;
+    pl.decode = pl.rows_max <= kDecodeRows && pl.kd == 128;
+    pl.BM = pl.decode ? kDecodeRows : fa::fwd_tile_rows(pl.kd);
+    pl.BN = pl.decode ? 32 : fa::fwd_tile_keys(pl.kd);
     pl.mt_max = (pl.rows_max + pl.BM - 1) / pl.BM;
     if (pl.mt_max < 1) pl.mt_max = 1;
     if (kind == FA_KIND_KVCACHE) {
@@ -225,7 +228,8 @@ void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
     pl.off_plse = off;
     if (pl.allow_split) off = align256(off + sizeof(float) * (size_t)pl.items_max * pl.BM);
     pl.off_po = off;
-    if (pl.allow_split) off = align256(off + sizeof(float) * (size_t)pl.items_max * pl.BM * p->headdim_v);
+    // partial rows are written at the kernel's head dim
+    if (pl.allow_split) off = align256(off + sizeof(float) * (size_t)pl.items_max * pl.BM * pl.kd);
     pl.off_qrot = off;
     // decode reads a rotated copy of q; prefill rotates q as it loads it
     if (pl.rotary && pl.decode) off = align256(off + 2 * (size_t)p->batch * p->seqlen_q * p->nheads * p->headdim);
@@ -408,14 +412,14 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
 
     mark(1);
     hipError_t e = pl.decode ? fa::launch_decode(a, p->dtype, pl.grid, stream)
-                             : fa::launch_fwd(a, p->dtype, 128, pl.grid, stream);
+                             : fa::launch_fwd(a, p->dtype, pl.kd, pl.grid, stream);
     if (e != hipSuccess) return fail(FA_EHIP, "attention launch failed: %s", hipGetErrorString(e));
     mark(2);
     if (pl.decode) {
         hipError_t em = fa::launch_decode_merge(a, p->dtype, pl.grid, stream);
         if (em != hipSuccess) return fail(FA_EHIP, "merge launch failed: %s", hipGetErrorString(em));
     } else if (pl.allow_split) {
-        hipError_t em = fa::launch_merge(a, p->dtype, 128, stream);
+        hipError_t em = fa::launch_merge(a, p->dtype, pl.kd, stream);
         if (em != hipSuccess) return fail(FA_EHIP, "merge launch failed: %s", hipGetErrorString(em));
     }
     mark(3);

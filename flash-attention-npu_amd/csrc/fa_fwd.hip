@@ -179,18 +179,26 @@ __device__ __forceinline__ const uint16_t* kv_row_ptr(const FwdArgs& a, const ui
 #define PF_NW 8
 #endif
 namespace pf {
-constexpr int D = 128;
-constexpr int RB = PF_RB;          // 16-row blocks per wave
-constexpr int NW = PF_NW;          // waves per workgroup
-constexpr int NT = NW * 64;
-constexpr int BM = NW * RB * 16;   // 256 packed rows per work tile
-constexpr int BN = 64;             // keys per LDS tile
-constexpr int DCH = D / 8;         // 16-byte chunks per key row
-constexpr int CPT = BN * DCH / NT; // chunks per thread per K (and per V) tile
-constexpr int KSTEPS = D / 32;
-constexpr int DBLK = D / 16;
 constexpr float kLazy = 8.f;       // log2 headroom before the running max moves
 }  // namespace pf
+
+// Tile shape per kernel head dim (128 or 256; smaller head dims run on the
+// 128 kernel with the dims above them read as zero). At 256 a wave keeps one
+// 16-row block: its q operands and O accumulators take twice the registers.
+template <int HD>
+struct PfCfg {
+    static constexpr int D = HD;
+    static constexpr int RB = HD > 128 ? 1 : PF_RB;   // 16-row blocks per wave
+    static constexpr int NW = PF_NW;                  // waves per workgroup
+    static constexpr int NT = NW * 64;
+    static constexpr int BM = NW * RB * 16;           // packed rows per work tile
+    static constexpr int BN = HD > 128 ? 32 : 64;     // keys per LDS tile (32-key halves)
+    static constexpr int VPRE = HD > 128 ? 8 : HD / 16; // V^T operands read ahead of the softmax
+    static constexpr int DCH = D / 8;                 // 16-byte chunks per key row
+    static constexpr int CPT = BN * DCH / NT;         // chunks per thread per K (and per V) tile
+    static constexpr int KSTEPS = D / 32;
+    static constexpr int DBLK = D / 16;
+};
 
 __device__ __forceinline__ int swz_k(int r, int c) { return c ^ (r & 15); }
 __device__ __forceinline__ int swz_v(int r, int c) { return c ^ ((r & 3) << 1) ^ (((r >> 2) & 1) << 3); }
@@ -198,9 +206,12 @@ __device__ __forceinline__ int swz_v(int r, int c) { return c ^ ((r & 3) << 1) ^
 // BIAS: softcap, ALiBi or a non-positive scale (scores are formed explicitly);
 // PAGED: K/V rows come through the block table; ROT: q is rotated (kvcache
 // rotary) as it is loaded.
-template <int DT, bool BIAS, bool PAGED, bool ROT>
-__global__ void __launch_bounds__(pf::NT, 1) fa_prefill_kernel(FwdArgs a) {
-    using namespace pf;
+template <int DT, int HD, bool BIAS, bool PAGED, bool ROT>
+__global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a) {
+    using C = PfCfg<HD>;
+    constexpr int D = C::D, RB = C::RB, NW = C::NW, NT = C::NT, BM = C::BM, BN = C::BN, DCH = C::DCH,
+                  CPT = C::CPT, KSTEPS = C::KSTEPS, DBLK = C::DBLK, VPRE = C::VPRE;
+    using pf::kLazy;
     __shared__ __attribute__((aligned(16))) uint16_t s_k[2][BN * D];
     __shared__ __attribute__((aligned(16))) uint16_t s_v[2][BN * D];
     __shared__ int s_pref[kMaxBatchLds + 1];
@@ -429,16 +440,18 @@ __global__ void __launch_bounds__(pf::NT, 1) fa_prefill_kernel(FwdArgs a) {
                 }
             }
             // V^T operands for this half tile (transpose reads), issued now so
-            // the LDS latency hides under the softmax below
-            u32x4 vt[DBLK];
-#pragma unroll
-            for (int db = 0; db < DBLK; ++db) {
+            // the LDS latency hides under the softmax below; past VPRE blocks
+            // (head dim 256) each read is issued one window ahead of its use
+            auto read_vt = [&](int db) {
                 const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_v[buf][offv[db] + (32 * hh) * D]);
                 const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_v[buf][offv[db] + (32 * hh + 16) * D]);
                 const u32x2 l2 = __builtin_bit_cast(u32x2, lo4);
                 const u32x2 h2 = __builtin_bit_cast(u32x2, hi4);
-                vt[db] = u32x4{l2[0], l2[1], h2[0], h2[1]};
-            }
+                return u32x4{l2[0], l2[1], h2[0], h2[1]};
+            };
+            u32x4 vt[VPRE];
+#pragma unroll
+            for (int db = 0; db < VPRE; ++db) vt[db] = read_vt(db);
             // scores (log2 units when BIAS; raw otherwise, scaled inside exp2's FMA)
             float xmax[RB];
             bool need = false;
@@ -507,9 +520,12 @@ __global__ void __launch_bounds__(pf::NT, 1) fa_prefill_kernel(FwdArgs a) {
             }
             // O^T += V^T . P^T
 #pragma unroll
-            for (int db = 0; db < DBLK; ++db)
+            for (int db = 0; db < DBLK; ++db) {
+                const u32x4 cur = vt[db % VPRE];
+                if (db + VPRE < DBLK) vt[db % VPRE] = read_vt(db + VPRE);
 #pragma unroll
-                for (int rb = 0; rb < RB; ++rb) oacc[rb][db] = mfma16x16x32<DT>(vt[db], pk[rb], oacc[rb][db]);
+                for (int rb = 0; rb < RB; ++rb) oacc[rb][db] = mfma16x16x32<DT>(cur, pk[rb], oacc[rb][db]);
+            }
         };
 
         if (ntiles > 0) {
@@ -526,7 +542,7 @@ __global__ void __launch_bounds__(pf::NT, 1) fa_prefill_kernel(FwdArgs a) {
             if (a.wl >= 0 && s1 - 1 < wi_lo + diag0 - a.wl) skip = true;
             if (!skip) {
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
+                for (int hh = 0; hh < BN / 32; ++hh) {
                     const int h0 = s0 + 32 * hh, h1 = h0 + 32;
                     bool hskip = false;
                     if (a.wr >= 0 && h0 > wi_hi + diag0 + a.wr) hskip = true;
@@ -687,39 +703,55 @@ __global__ void __launch_bounds__(256) fa_combine_flat_kernel(const float* __res
 }
 
 // ---- host-side launchers (called from fa_api.cpp) -------------------------------------
-int fwd_tile_rows() { return pf::BM; }
-int fwd_tile_keys() { return pf::BN; }
+int fwd_tile_rows(int d) { return d > 128 ? PfCfg<256>::BM : PfCfg<128>::BM; }
+int fwd_tile_keys(int d) { return d > 128 ? PfCfg<256>::BN : PfCfg<128>::BN; }
 
-template <int DT, bool BIAS, bool ROT>
+template <int DT, int HD, bool BIAS, bool ROT>
 static void launch_prefill_r(const FwdArgs& a, int grid, hipStream_t stream) {
-    if (a.block_table) hipLaunchKernelGGL((fa_prefill_kernel<DT, BIAS, true, ROT>), dim3(grid), dim3(pf::NT), 0, stream, a);
-    else hipLaunchKernelGGL((fa_prefill_kernel<DT, BIAS, false, ROT>), dim3(grid), dim3(pf::NT), 0, stream, a);
+    constexpr int NT = PfCfg<HD>::NT;
+    if (a.block_table) hipLaunchKernelGGL((fa_prefill_kernel<DT, HD, BIAS, true, ROT>), dim3(grid), dim3(NT), 0, stream, a);
+    else hipLaunchKernelGGL((fa_prefill_kernel<DT, HD, BIAS, false, ROT>), dim3(grid), dim3(NT), 0, stream, a);
 }
 
-template <int DT, bool BIAS>
+template <int DT, int HD, bool BIAS>
 static void launch_prefill_b(const FwdArgs& a, int grid, hipStream_t stream) {
-    if (a.rot_cos) launch_prefill_r<DT, BIAS, true>(a, grid, stream);
-    else launch_prefill_r<DT, BIAS, false>(a, grid, stream);
+    if (a.rot_cos) launch_prefill_r<DT, HD, BIAS, true>(a, grid, stream);
+    else launch_prefill_r<DT, HD, BIAS, false>(a, grid, stream);
 }
 
-hipError_t launch_fwd(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream) {
-    if (d != 128) return hipErrorInvalidValue;
+template <int HD>
+static void launch_prefill_d(const FwdArgs& a, int dtype, int grid, hipStream_t stream) {
     const bool bias = a.softcap > 0.f || a.alibi != nullptr || !(a.scale > 0.f);
     if (dtype == DT_BF16) {
-        if (bias) launch_prefill_b<DT_BF16, true>(a, grid, stream);
-        else launch_prefill_b<DT_BF16, false>(a, grid, stream);
+        if (bias) launch_prefill_b<DT_BF16, HD, true>(a, grid, stream);
+        else launch_prefill_b<DT_BF16, HD, false>(a, grid, stream);
     } else {
-        if (bias) launch_prefill_b<DT_FP16, true>(a, grid, stream);
-        else launch_prefill_b<DT_FP16, false>(a, grid, stream);
+        if (bias) launch_prefill_b<DT_FP16, HD, true>(a, grid, stream);
+        else launch_prefill_b<DT_FP16, HD, false>(a, grid, stream);
     }
+}
+
+// d: the kernel head dim, 128 or 256 (a.hd <= d is the head dim in memory)
+hipError_t launch_fwd(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream) {
+    if (d == 128) launch_prefill_d<128>(a, dtype, grid, stream);
+    else if (d == 256) launch_prefill_d<256>(a, dtype, grid, stream);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
+template <int HD>
+static void launch_merge_d(const FwdArgs& a, int dtype, hipStream_t stream) {
+    constexpr int BM = PfCfg<HD>::BM;
+    constexpr int RPB = 256 / (HD / 8);
+    const int64_t grid = (int64_t)a.B * a.mt_max * a.Hk * ((BM + RPB - 1) / RPB);
+    if (dtype == DT_BF16) hipLaunchKernelGGL((fa_merge_kernel<DT_BF16, HD, BM>), dim3(grid), dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((fa_merge_kernel<DT_FP16, HD, BM>), dim3(grid), dim3(256), 0, stream, a);
+}
+
 hipError_t launch_merge(const FwdArgs& a, int dtype, int d, hipStream_t stream) {
-    if (d != 128) return hipErrorInvalidValue;
-    const int64_t grid = (int64_t)a.B * a.mt_max * a.Hk * (pf::BM / 16);
-    if (dtype == DT_BF16) hipLaunchKernelGGL((fa_merge_kernel<DT_BF16, 128, pf::BM>), dim3(grid), dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((fa_merge_kernel<DT_FP16, 128, pf::BM>), dim3(grid), dim3(256), 0, stream, a);
+    if (d == 128) launch_merge_d<128>(a, dtype, stream);
+    else if (d == 256) launch_merge_d<256>(a, dtype, stream);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

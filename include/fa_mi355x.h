@@ -66,7 +66,7 @@ typedef struct fa_fwd_params {
     int32_t seqlen_q;     /* Sq (dense/kvcache), max_seqlen_q (varlen) */
     int32_t nheads;       /* H */
     int32_t nheads_k;     /* Hk, H % Hk == 0 */
-    int32_t headdim;      /* D */
+    int32_t headdim;      /* D: a multiple of 8, at most 256 */
     int32_t headdim_v;    /* Dv (must equal D) */
     int32_t seqlen_k;     /* dense: Sk; kvcache contiguous: seqlen_cache; varlen: max_seqlen_k */
     int32_t batch_cache;  /* kvcache contiguous: rows of k/v cache; paged: num_blocks */

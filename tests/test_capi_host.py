@@ -77,7 +77,7 @@ def _valid(capi, **kw):
 
 def test_validate_accepts_a_valid_call(capi):
     assert capi.validate(_valid(capi), capi.FA_KIND_KVCACHE) == capi.FA_OK
-    for d in (8, 64, 96, 128):
+    for d in (8, 64, 96, 128, 136, 192, 256):
         assert capi.validate(_valid(capi, headdim=d, headdim_v=d), capi.FA_KIND_DENSE) == capi.FA_OK, d
     assert capi.validate(_valid(capi, k_new=0x70000, v_new=0x80000, seqlen_new=1, knew_batch_stride=256,
                                 knew_row_stride=256, knew_head_stride=128, vnew_batch_stride=256,
@@ -89,7 +89,7 @@ BAD = [
     (dict(abi_version=7), 0, "EINVAL", "abi_version"),
     (dict(dtype=2), 0, "EINVAL", "only support fp16 and bf16"),
     (dict(nheads=6, nheads_k=4), 0, "EINVAL", "must divide number of heads in query"),
-    (dict(headdim=256, headdim_v=256), 0, "EUNSUPPORTED", "headdim 256"),
+    (dict(headdim=264, headdim_v=264), 0, "EINVAL", "at most 256"),
     (dict(headdim=60, headdim_v=60), 0, "EINVAL", "multiple of 8"),
     (dict(dropout_p=0.1), 1, "EUNSUPPORTED", "dropout"),
     (dict(q=0x10008), 0, "EINVAL", "16-byte aligned"),

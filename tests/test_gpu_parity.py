@@ -213,6 +213,69 @@ def test_headdim_chunked_prefill_rotary(rotary):
     run_kvcache(2, 80, 16, 4, 64, torch.bfloat16, 400, [200, 57], s_new=80, rotary=rotary, causal=True, seed=53)
 
 
+# ---- head dims above 128: the 256 prefill kernel (decode shapes run on it too) --------------
+@pytest.mark.parametrize("D", [136, 192, 256])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_headdim_large_dense(D, dtype):
+    print(f"case headdim dense D={D} {dtype}", flush=True)
+    run_dense(2, 150, 260, 8, 2, D, dtype, causal=True, seed=60 + D)
+
+
+def test_headdim_256_dense_window_softcap_alibi():
+    print("case headdim 256 dense window softcap alibi", flush=True)
+    run_dense(2, 200, 333, 8, 4, 256, torch.bfloat16, causal=False, window=(90, 30), softcap=30.0, alibi=True,
+              seed=61)
+
+
+@pytest.mark.parametrize("D", [192, 256])
+def test_headdim_large_decode_paged_append(D):
+    # reference v3 decode cases at D=256 (tests/test_flash_attn_npu_v3.py:193,207)
+    print(f"case headdim {D} decode paged append", flush=True)
+    run_kvcache(5, 1, 32, 8, D, torch.bfloat16, 0, [700, 33, 4000, 1, 2500], s_new=1, page=64, causal=True,
+                seed=62 + D)
+
+
+def test_headdim_256_decode_contiguous_long():
+    print("case headdim 256 decode contiguous long (split)", flush=True)
+    run_kvcache(2, 1, 64, 8, 256, torch.bfloat16, 4096, [4000, 2048], s_new=1, causal=True, seed=63)
+
+
+def test_headdim_256_spec_verify_window_alibi_batchidx():
+    print("case headdim 256 verify paged window alibi batch_idx", flush=True)
+    run_kvcache(4, 13, 32, 8, 256, torch.bfloat16, 0, [1500, 2600, 900, 3000], s_new=0, page=128, causal=True,
+                window=(600, 0), alibi=True, batch_idx=True, seed=64)
+
+
+@pytest.mark.parametrize("rotary", ["neox", "interleaved", "partial"])
+def test_headdim_256_chunked_prefill_rotary(rotary):
+    print(f"case headdim 256 chunked prefill rotary {rotary}", flush=True)
+    run_kvcache(2, 70, 16, 4, 256, torch.bfloat16, 400, [200, 57], s_new=70, rotary=rotary, causal=True, seed=65)
+
+
+def test_headdim_256_varlen():
+    import flash_attn_npu_v3
+    print("case headdim 256 varlen", flush=True)
+    g = _gen(66)
+    dtype = torch.bfloat16
+    H, Hk, D = 8, 2, 256
+    lq = [37, 1, 300, 64]
+    lk = [37, 90, 300, 700]
+    cq = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
+    ck = np.concatenate([[0], np.cumsum(lk)]).astype(np.int32)
+    q = randn((cq[-1], H, D), dtype, g, "cpu")
+    k = randn((ck[-1], Hk, D), dtype, g, "cpu")
+    v = randn((ck[-1], Hk, D), dtype, g, "cpu")
+    ref_out, ref_lse = orc.attention(bits(q).reshape(q.shape), bits(k).reshape(k.shape), bits(v).reshape(v.shape),
+                                     dtype=odt(dtype), scale=D ** -0.5, causal=True, cu_seqlens_q=cq,
+                                     cu_seqlens_k=ck, max_seqlen_q=max(lq), nthreads=NT)
+    out, lse = flash_attn_npu_v3.flash_attn_varlen_func(
+        q.to(DEV), k.to(DEV), v.to(DEV), torch.from_numpy(cq).to(DEV), torch.from_numpy(ck).to(DEV), max(lq),
+        max(lk), causal=True, return_attn_probs=True)
+    torch.cuda.synchronize()
+    assert_close_out(out, ref_out, dtype)
+    assert_close_lse(lse, ref_lse)
+
+
 def test_headdim_padded_to_multiple_of_8():
     # the v2 API pads the head dim to a multiple of 8 and slices the output (interface_arch22.py:1102-1176)
     import flash_attn_npu_v2
