@@ -32,6 +32,9 @@ hipError_t launch_decode_merge(const FwdArgs& a, int dtype, int grid, hipStream_
 hipError_t launch_combine_flat(const float* po, const float* pl, int S, int64_t R, int Dv, void* out, int64_t ors,
                                int out_dtype, float* lse, hipStream_t stream);
 hipError_t launch_kv_prep(const KvPrepArgs& a, int dtype, hipStream_t stream);
+hipError_t launch_bwd(const BwdArgs& a, int dtype, int d, int grid_kv, int grid_q, hipStream_t stream);
+int bwd_key_block(int d);
+int bwd_row_block(int d);
 }  // namespace fa
 
 namespace {
@@ -426,6 +429,133 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
     return FA_OK;
 }
 
+// ---- backward ---------------------------------------------------------------------------
+// Checks of mha_bwd / mha_varlen_bwd (flash_api.cpp:1063-1299 of the reference),
+// with this build's layout rules (16-byte rows, strides in multiples of 8).
+fa_status_t validate_bwd(const fa_bwd_params* p, int kind) {
+    FA_CHECK(p != nullptr, "params must not be null");
+    FA_CHECK(p->abi_version == FA_MI355X_ABI_VERSION, "abi_version %d does not match library ABI %d", p->abi_version,
+             FA_MI355X_ABI_VERSION);
+    FA_CHECK(kind == FA_KIND_DENSE || kind == FA_KIND_VARLEN, "backward kind must be dense or varlen, got %d", kind);
+    FA_CHECK(p->dtype == FA_DTYPE_FP16 || p->dtype == FA_DTYPE_BF16,
+             "FlashAttention only support fp16 and bf16 data type");
+    FA_CHECK(p->batch >= 1, "batch size must be positive");
+    FA_CHECK(p->batch <= kMaxBatch, "batch size %d exceeds the supported maximum %d", p->batch, kMaxBatch);
+    FA_CHECK(p->nheads >= 1 && p->nheads_k >= 1, "number of heads must be positive");
+    FA_CHECK(p->nheads % p->nheads_k == 0, "Number of heads in key/value must divide number of heads in query");
+    FA_CHECK(p->headdim >= 1 && p->headdim % 8 == 0, "head dimension must be a positive multiple of 8");
+    FA_CHECK(p->headdim <= 256, "FlashAttention only supports head dimension at most 256");
+    if (p->headdim > 128)
+        return fail(FA_EUNSUPPORTED, "backward supports head dimensions up to 128 in this build, got %d", p->headdim);
+    if (p->dropout_p != 0.f) return fail(FA_EUNSUPPORTED, "dropout is not supported");
+    FA_CHECK(p->softcap >= 0.f, "softcap must be non-negative (0.0 disables softcap)");
+    FA_CHECK(p->seqlen_q >= 0 && p->seqlen_k >= 0, "sequence lengths must be >= 0");
+    FA_CHECK(p->q && p->k && p->v && p->out && p->dout && p->dq && p->dk && p->dv,
+             "q, k, v, out, dout, dq, dk and dv must be given");
+    FA_CHECK(p->softmax_lse && p->softmax_d, "softmax_lse and softmax_d must be given");
+    FA_CHECK(aligned16(p->q) && aligned16(p->k) && aligned16(p->v) && aligned16(p->out) && aligned16(p->dout) &&
+                 aligned16(p->dq) && aligned16(p->dk) && aligned16(p->dv),
+             "q, k, v, out, dout, dq, dk and dv must be 16-byte aligned");
+    FA_CHECK(strides8(p->q_batch_stride, p->q_row_stride, p->q_head_stride) &&
+                 strides8(p->k_batch_stride, p->k_row_stride, p->k_head_stride) &&
+                 strides8(p->v_batch_stride, p->v_row_stride, p->v_head_stride) &&
+                 strides8(p->out_batch_stride, p->out_row_stride, p->out_head_stride) &&
+                 strides8(p->dout_batch_stride, p->dout_row_stride, p->dout_head_stride) &&
+                 strides8(p->dq_batch_stride, p->dq_row_stride, p->dq_head_stride) &&
+                 strides8(p->dk_batch_stride, p->dk_row_stride, p->dk_head_stride) &&
+                 strides8(p->dv_batch_stride, p->dv_row_stride, p->dv_head_stride),
+             "strides must be multiples of 8 elements");
+    if (p->alibi_slopes)
+        FA_CHECK(p->alibi_batch_stride == 0 || p->alibi_batch_stride == p->nheads,
+                 "alibi_slopes must have shape (nheads) or (batch_size, nheads)");
+    if (kind == FA_KIND_VARLEN) {
+        FA_CHECK(p->cu_seqlens_q && p->cu_seqlens_k, "cu_seqlens_q and cu_seqlens_k are required for varlen");
+        FA_CHECK(p->total_q >= 0, "total_q must be >= 0");
+    } else {
+        FA_CHECK(!p->cu_seqlens_q && !p->cu_seqlens_k, "cu_seqlens are only valid for varlen");
+    }
+    return FA_OK;
+}
+
+fa_status_t run_backward(const fa_bwd_params* p, int kind, void* stream_v) {
+    fa_status_t st = validate_bwd(p, kind);
+    if (st != FA_OK) return st;
+    if (p->seqlen_q == 0 || (kind == FA_KIND_VARLEN && p->total_q == 0)) return FA_OK;
+    fa::BwdArgs a{};
+    a.q = p->q;
+    a.q_sb = p->q_batch_stride;
+    a.q_si = p->q_row_stride;
+    a.q_sh = p->q_head_stride;
+    a.k = p->k;
+    a.k_sb = p->k_batch_stride;
+    a.k_si = p->k_row_stride;
+    a.k_sh = p->k_head_stride;
+    a.v = p->v;
+    a.v_sb = p->v_batch_stride;
+    a.v_si = p->v_row_stride;
+    a.v_sh = p->v_head_stride;
+    a.out = p->out;
+    a.o_sb = p->out_batch_stride;
+    a.o_si = p->out_row_stride;
+    a.o_sh = p->out_head_stride;
+    a.dout = p->dout;
+    a.do_sb = p->dout_batch_stride;
+    a.do_si = p->dout_row_stride;
+    a.do_sh = p->dout_head_stride;
+    a.dq = p->dq;
+    a.dq_sb = p->dq_batch_stride;
+    a.dq_si = p->dq_row_stride;
+    a.dq_sh = p->dq_head_stride;
+    a.dk = p->dk;
+    a.dk_sb = p->dk_batch_stride;
+    a.dk_si = p->dk_row_stride;
+    a.dk_sh = p->dk_head_stride;
+    a.dv = p->dv;
+    a.dv_sb = p->dv_batch_stride;
+    a.dv_si = p->dv_row_stride;
+    a.dv_sh = p->dv_head_stride;
+    a.lse = p->softmax_lse;
+    a.dsum = p->softmax_d;
+    if (kind == FA_KIND_VARLEN) {
+        a.lse_sb = 0;
+        a.lse_sh = p->total_q;
+    } else {
+        a.lse_sb = (int64_t)p->nheads * p->seqlen_q;
+        a.lse_sh = p->seqlen_q;
+    }
+    a.cu_seqlens_q = kind == FA_KIND_VARLEN ? p->cu_seqlens_q : nullptr;
+    a.cu_seqlens_k = kind == FA_KIND_VARLEN ? p->cu_seqlens_k : nullptr;
+    a.alibi = p->alibi_slopes;
+    a.alibi_sb = p->alibi_batch_stride;
+    a.scale = p->softmax_scale;
+    a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
+    a.softcap = p->softcap;
+    a.B = p->batch;
+    a.Sq = p->seqlen_q;
+    a.Sk = p->seqlen_k;
+    a.H = p->nheads;
+    a.Hk = p->nheads_k;
+    a.g = p->nheads / p->nheads_k;
+    a.hd = p->headdim;
+    a.total_q = p->total_q;
+    // window normalisation as in the forward (flash_api.cpp:483-494)
+    int wl = p->window_size_left < 0 ? -1 : p->window_size_left;
+    int wr = p->window_size_right < 0 ? -1 : p->window_size_right;
+    if (p->is_causal) wr = 0;
+    a.wl = wl;
+    a.wr = wr;
+    const int kd = 128;
+    const int64_t gkv = (int64_t)p->batch * p->nheads_k * ((p->seqlen_k + fa::bwd_key_block(kd) - 1) / fa::bwd_key_block(kd));
+    const int64_t gq = (int64_t)p->batch * p->nheads_k *
+                       (((int64_t)p->seqlen_q * a.g + fa::bwd_row_block(kd) - 1) / fa::bwd_row_block(kd));
+    const int cap = 16 * cu_count();  // the kernels walk their work items in a grid-stride loop
+    const int grid_kv = (int)std::max<int64_t>(1, std::min<int64_t>(gkv, cap));
+    const int grid_q = (int)std::max<int64_t>(1, std::min<int64_t>(gq, cap));
+    hipError_t e = fa::launch_bwd(a, p->dtype, kd, grid_kv, grid_q, static_cast<hipStream_t>(stream_v));
+    if (e != hipSuccess) return fail(FA_EHIP, "backward launch failed: %s", hipGetErrorString(e));
+    return FA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -469,5 +599,19 @@ fa_status_t fa_combine(const float* out_partial, const float* lse_partial, int32
     if (e != hipSuccess) return fail(FA_EHIP, "combine launch failed: %s", hipGetErrorString(e));
     return FA_OK;
 }
+
+fa_status_t fa_validate_bwd(const fa_bwd_params* p, int32_t kind) { return validate_bwd(p, kind); }
+
+fa_status_t fa_bwd_workspace_size(const fa_bwd_params* p, int32_t kind, size_t* bytes) {
+    if (!bytes) return fail(FA_EINVAL, "bytes must not be null");
+    fa_status_t st = validate_bwd(p, kind);
+    if (st != FA_OK) return st;
+    *bytes = 0;
+    return FA_OK;
+}
+
+fa_status_t fa_mha_bwd(const fa_bwd_params* p, void* stream) { return run_backward(p, FA_KIND_DENSE, stream); }
+
+fa_status_t fa_mha_varlen_bwd(const fa_bwd_params* p, void* stream) { return run_backward(p, FA_KIND_VARLEN, stream); }
 
 }  // extern "C"

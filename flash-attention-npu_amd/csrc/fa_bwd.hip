@@ -1,0 +1,692 @@
+// fa_bwd.hip -- FlashAttention backward (dense / varlen) for gfx950 (MI355X).
+//
+// Reference behaviour being reproduced (paths relative to the reference repo):
+//   mha_bwd / mha_varlen_bwd       csrc/arch22/flash_attn_npu_v2/flash_api.cpp:1063-1299
+//   FAG kernel (launch_fag_general) csrc/arch22/flash_attn_npu_v2/fag_general_host.cpp
+//   golden                          tests/fa_small_op_golden.py:85-353
+// Given q, k, v, out, dout and the forward's log-sum-exp, with P recomputed as
+// exp(s - lse) (s the scaled, optionally soft-capped and ALiBi-biased score):
+//   dsum_i = sum_d dout[i,d] * out[i,d]
+//   dV = P^T dout,  dP = dout V^T,  dS = P * (dP - dsum) * scale [* (1 - tanh^2)]
+//   dQ = dS K,      dK = dS^T Q
+// (the golden's rowsum(dP * P) equals dsum up to the rounding of out).
+//
+// MI355X design: three launches, no atomics, so results are deterministic.
+//   * fa_bwd_dsum_kernel: dsum per (row, head), also returned as softmax_d.
+//   * fa_bwd_dkdv_kernel: one workgroup per (batch, kv head, 128-key block);
+//     each of 8 waves keeps 16 keys' K and V in registers as MFMA B operands
+//     and streams the packed (query, head) rows of all g query heads through
+//     double-buffered LDS tiles of 64 rows. S = Q.K^T and dP = dO.V^T land
+//     with one key and 8 rows per lane, exactly the packed operand of
+//     dV^T += dO^T.P and dK^T += Q^T.dS, whose dO^T / Q^T operands are
+//     transpose reads (ds_read_b64_tr_b16) of the same tiles. GQA needs no
+//     reduction: the g heads of a kv head are rows of the same work item.
+//   * fa_bwd_dq_kernel: the forward's shape (8 waves x 16 packed rows, 64-key
+//     LDS tiles): S^T = K.Q^T and dP^T = V.dO^T with q and dout in registers,
+//     then dQ^T += K^T.dS^T with K^T by transpose reads.
+// dS and P are rounded to the input type before their MFMAs.
+#include "fa_common.h"
+#include "fa_kernel_args.h"
+
+#include <type_traits>
+
+namespace fa {
+
+namespace bw {
+constexpr int kMaxBatch = 2048;
+constexpr int NW = 8;
+constexpr int NT = NW * 64;
+}  // namespace bw
+
+template <int HD>
+struct BwCfg {
+    static constexpr int D = HD;
+    static constexpr int DCH = D / 8;
+    static constexpr int KSTEPS = D / 32;
+    static constexpr int DBLK = D / 16;
+    // dK/dV kernel: 16 keys per wave, q tiles of 64 packed rows
+    static constexpr int BK = bw::NW * 16;
+    static constexpr int BQ = 64;
+    static constexpr int CPQ = BQ * DCH / bw::NT;  // chunks per thread per q (and dout) tile
+    // dQ kernel: 1 row block of 16 per wave (q, dout and dQ^T of two would
+    // not fit 256 VGPRs), key tiles of 64
+    static constexpr int RB = 1;
+    static constexpr int BM = bw::NW * RB * 16;
+    static constexpr int BN = 64;
+    static constexpr int CPK = BN * DCH / bw::NT;
+};
+
+struct BwBatch {
+    int sq, sk, rows;  // query positions, keys, packed rows (sq * g)
+};
+
+__device__ __forceinline__ BwBatch bw_batch(const BwdArgs& a, int b) {
+    BwBatch r;
+    int sq = a.cu_seqlens_q ? a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b] : a.Sq;
+    int sk = a.cu_seqlens_k ? a.cu_seqlens_k[b + 1] - a.cu_seqlens_k[b] : a.Sk;
+    r.sq = min(max(sq, 0), a.Sq);
+    r.sk = min(max(sk, 0), a.Sk);
+    r.rows = r.sq * a.g;
+    return r;
+}
+
+// Per-batch item prefix in LDS (s_pref[0..B]); items(b) is the work item
+// count of batch b. Every workgroup computes the same table.
+template <class F>
+__device__ __forceinline__ int bw_prefix(const BwdArgs& a, int* s_pref, F items) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int b = tid; b < a.B; b += bw::NT) s_pref[b + 1] = items(b);
+    __syncthreads();
+    if (wave == 0) {
+        const int seg = (a.B + 63) / 64, b0 = lane * seg;
+        int local = 0;
+        for (int k = 0; k < seg; ++k)
+            if (b0 + k < a.B) local += s_pref[b0 + k + 1];
+        int incl = local;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            int v = __shfl_up(incl, o);
+            if (lane >= o) incl += v;
+        }
+        int run = incl - local;
+        for (int k = 0; k < seg; ++k)
+            if (b0 + k < a.B) {
+                run += s_pref[b0 + k + 1];
+                s_pref[b0 + k + 1] = run;
+            }
+        if (lane == 0) s_pref[0] = 0;
+    }
+    __syncthreads();
+    return s_pref[a.B];
+}
+
+__device__ __forceinline__ int bw_find_batch(const int* s_pref, int B, int w) {
+    int bl = 0, bh = B;
+    while (bh - bl > 1) {
+        const int mid = (bl + bh) >> 1;
+        if (s_pref[mid] <= w) bl = mid;
+        else bh = mid;
+    }
+    return bl;
+}
+
+// Score in log2 units from the raw dot product x: scale, optional soft cap
+// (t returned for its derivative), optional ALiBi bias.
+template <bool BIAS>
+__device__ __forceinline__ float bw_score(const BwdArgs& a, float x, float slope, int dist, float& t) {
+    if constexpr (BIAS) {
+        float y = x * a.scale;
+        t = 0.f;
+        if (a.softcap > 0.f) {
+            t = tanhf(y / a.softcap);
+            y = a.softcap * t;
+        }
+        if (a.alibi) y -= slope * (float)(dist < 0 ? -dist : dist);
+        return y * kLog2e;
+    } else {
+        t = 0.f;
+        return x * a.scale_log2;
+    }
+}
+
+// ---- dsum = rowsum(dout * out) -------------------------------------------------------------
+// One 16-lane group per (token, head) row over up to 256 dims (16 dims per lane).
+__global__ void __launch_bounds__(256) fa_bwd_dsum_kernel(BwdArgs a, int dt) {
+    const int grp = threadIdx.x >> 4, l16 = threadIdx.x & 15;
+    const int64_t row = (int64_t)blockIdx.x * 16 + grp;  // token * H + head
+    const int64_t ntok = a.cu_seqlens_q ? (int64_t)a.total_q : (int64_t)a.B * a.Sq;
+    if (row >= ntok * a.H) return;
+    const int h = (int)(row % a.H);
+    const int64_t tok = row / a.H;
+    int64_t oo, od, lo;
+    if (a.cu_seqlens_q) {
+        oo = tok * a.o_si + (int64_t)h * a.o_sh;
+        od = tok * a.do_si + (int64_t)h * a.do_sh;
+        lo = (int64_t)h * a.lse_sh + tok;
+    } else {
+        const int64_t b = tok / a.Sq, i = tok % a.Sq;
+        oo = b * a.o_sb + i * a.o_si + (int64_t)h * a.o_sh;
+        od = b * a.do_sb + i * a.do_si + (int64_t)h * a.do_sh;
+        lo = b * a.lse_sb + (int64_t)h * a.lse_sh + i;
+    }
+    const uint16_t* o = static_cast<const uint16_t*>(a.out) + oo;
+    const uint16_t* d = static_cast<const uint16_t*>(a.dout) + od;
+    float acc = 0.f;
+    for (int c = l16; c * 8 < a.hd; c += 16) {
+        const u32x4 ov = *reinterpret_cast<const u32x4*>(o + c * 8);
+        const u32x4 dv = *reinterpret_cast<const u32x4*>(d + c * 8);
+        uint16_t oh[8], dh[8];
+        __builtin_memcpy(oh, &ov, 16);
+        __builtin_memcpy(dh, &dv, 16);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float x = dt == DT_BF16 ? f16_to_32<DT_BF16>(oh[e]) : f16_to_32<DT_FP16>(oh[e]);
+            const float y = dt == DT_BF16 ? f16_to_32<DT_BF16>(dh[e]) : f16_to_32<DT_FP16>(dh[e]);
+            acc += x * y;
+        }
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) acc += __shfl_xor(acc, m);
+    if (l16 == 0) a.dsum[lo] = acc;
+}
+
+// ---- dK, dV ---------------------------------------------------------------------------------
+template <int DT, int HD, bool BIAS>
+__global__ void __launch_bounds__(bw::NT, 1) fa_bwd_dkdv_kernel(BwdArgs a) {
+    using C = BwCfg<HD>;
+    constexpr int D = C::D, DCH = C::DCH, KSTEPS = C::KSTEPS, DBLK = C::DBLK, BK = C::BK, BQ = C::BQ,
+                  CPQ = C::CPQ, NT = bw::NT;
+    __shared__ __attribute__((aligned(16))) uint16_t s_q[2][BQ * D];
+    __shared__ __attribute__((aligned(16))) uint16_t s_do[2][BQ * D];
+    __shared__ __attribute__((aligned(16))) float s_lse[2][BQ];   // lse * log2(e); +inf for rows past the end
+    __shared__ __attribute__((aligned(16))) float s_ds[2][BQ];    // dsum
+    __shared__ __attribute__((aligned(16))) float s_sl[2][BQ];    // ALiBi slope of the row's head
+    __shared__ __attribute__((aligned(16))) int s_pos[2][BQ];     // query position; -1 past the end
+    __shared__ int s_pref[bw::kMaxBatch + 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, G = lane >> 4;
+    const int total = bw_prefix(a, s_pref, [&](int b) {
+        const BwBatch bb = bw_batch(a, b);
+        return a.Hk * ((bb.sk + BK - 1) / BK);
+    });
+
+    // LDS offsets: row reads (A operands) and transpose reads, both on the
+    // swz_v layout; staging stores
+    int offr[KSTEPS];
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) offr[s] = li * D + (swz_v(li, G * KSTEPS + s) << 3);
+    const int r4 = li >> 2, c4 = li & 3;
+    int offt[DBLK];
+#pragma unroll
+    for (int db = 0; db < DBLK; ++db)
+        offt[db] = (4 * G + r4) * D + (swz_v(4 * G + r4, 2 * db + (c4 >> 1)) << 3) + (c4 & 1) * 4;
+    const int dch = tid % DCH, rr0 = tid / DCH;
+
+    const uint16_t* qp = static_cast<const uint16_t*>(a.q);
+    const uint16_t* kp = static_cast<const uint16_t*>(a.k);
+    const uint16_t* vp = static_cast<const uint16_t*>(a.v);
+    const uint16_t* dop = static_cast<const uint16_t*>(a.dout);
+
+    for (int w = blockIdx.x; w < total; w += gridDim.x) {
+        const int b = bw_find_batch(s_pref, a.B, w);
+        const BwBatch bb = bw_batch(a, b);
+        const int local = w - s_pref[b];
+        const int hk = local % a.Hk;
+        const int kt = local / a.Hk;
+        const int j0 = kt * BK;
+        const int g = a.g;
+        const int diag0 = bb.sk - bb.sq;
+        const int64_t qbase = a.cu_seqlens_q ? (int64_t)a.cu_seqlens_q[b] * a.q_si : (int64_t)b * a.q_sb;
+        const int64_t dobase = a.cu_seqlens_q ? (int64_t)a.cu_seqlens_q[b] * a.do_si : (int64_t)b * a.do_sb;
+        const int64_t kbase = a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.k_si : (int64_t)b * a.k_sb;
+        const int64_t vbase = a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.v_si : (int64_t)b * a.v_sb;
+
+        // this wave's 16 keys as B operands: lane holds key (j0 + 16*wave + li), chunk G*KSTEPS + s
+        const int jw = j0 + 16 * wave;
+        const int jl = jw + li;
+        u32x4 kreg[KSTEPS], vreg[KSTEPS];
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+            const int c = G * KSTEPS + s;
+            const bool in = jl < bb.sk && c * 8 < a.hd;
+            kreg[s] = in ? *reinterpret_cast<const u32x4*>(kp + kbase + (int64_t)jl * a.k_si + (int64_t)hk * a.k_sh + c * 8)
+                         : u32x4{0u, 0u, 0u, 0u};
+            vreg[s] = in ? *reinterpret_cast<const u32x4*>(vp + vbase + (int64_t)jl * a.v_si + (int64_t)hk * a.v_sh + c * 8)
+                         : u32x4{0u, 0u, 0u, 0u};
+        }
+
+        // packed rows that can see any key of [j0, j0 + BK)
+        int i_lo = 0, i_hi = bb.sq - 1;
+        if (a.wr >= 0) i_lo = max(0, j0 - diag0 - a.wr);
+        if (a.wl >= 0) i_hi = min(bb.sq - 1, j0 + BK - 1 - diag0 + a.wl);
+        const int r_lo = i_lo * g;
+        const int r_hi = (i_hi >= i_lo) ? (i_hi + 1) * g : r_lo;
+        const int ntiles = (r_hi - r_lo + BQ - 1) / BQ;
+        // the same range for this wave's 16 keys (skips tiles it cannot see)
+        int wi_lo = 0, wi_hi = bb.sq - 1;
+        if (a.wr >= 0) wi_lo = max(0, jw - diag0 - a.wr);
+        if (a.wl >= 0) wi_hi = min(bb.sq - 1, jw + 15 - diag0 + a.wl);
+        const bool wave_live = jw < bb.sk;
+
+        f32x4 dka[DBLK], dva[DBLK];
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db) {
+            dka[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+            dva[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+
+        u32x4 qr[CPQ], dr[CPQ];
+        float lr = 0.f, dsr = 0.f, slr = 0.f;
+        int pr = -1;
+        auto load_tile = [&](int r0) {
+#pragma unroll
+            for (int u = 0; u < CPQ; ++u) {
+                const int r = r0 + rr0 + u * (NT / DCH);
+                if (r < r_hi && dch * 8 < a.hd) {
+                    const int i = r / g, h = hk * g + r % g;
+                    qr[u] = *reinterpret_cast<const u32x4*>(qp + qbase + (int64_t)i * a.q_si + (int64_t)h * a.q_sh + dch * 8);
+                    dr[u] = *reinterpret_cast<const u32x4*>(dop + dobase + (int64_t)i * a.do_si + (int64_t)h * a.do_sh + dch * 8);
+                } else {
+                    qr[u] = u32x4{0u, 0u, 0u, 0u};
+                    dr[u] = u32x4{0u, 0u, 0u, 0u};
+                }
+            }
+            if (tid < BQ) {
+                const int r = r0 + tid;
+                if (r < r_hi) {
+                    const int i = r / g, h = hk * g + r % g;
+                    const int64_t lo = a.cu_seqlens_q ? (int64_t)h * a.lse_sh + a.cu_seqlens_q[b] + i
+                                                      : (int64_t)b * a.lse_sb + (int64_t)h * a.lse_sh + i;
+                    lr = a.lse[lo] * kLog2e;
+                    dsr = a.dsum[lo];
+                    slr = (BIAS && a.alibi) ? a.alibi[(int64_t)b * a.alibi_sb + h] : 0.f;
+                    pr = i;
+                } else {
+                    lr = INFINITY;
+                    dsr = 0.f;
+                    slr = 0.f;
+                    pr = -1;
+                }
+            }
+        };
+        auto store_tile = [&](int buf) {
+#pragma unroll
+            for (int u = 0; u < CPQ; ++u) {
+                const int r = rr0 + u * (NT / DCH);
+                const int off = r * D + (swz_v(r, dch) << 3);
+                *reinterpret_cast<u32x4*>(&s_q[buf][off]) = qr[u];
+                *reinterpret_cast<u32x4*>(&s_do[buf][off]) = dr[u];
+            }
+            if (tid < BQ) {
+                s_lse[buf][tid] = lr;
+                s_ds[buf][tid] = dsr;
+                s_sl[buf][tid] = slr;
+                s_pos[buf][tid] = pr;
+            }
+        };
+
+        // 32 rows (half tile hh) against this wave's 16 keys
+        auto half = [&](int buf, int hh, int rbase, auto mask_tag) {
+            constexpr bool MASK = decltype(mask_tag)::value;
+            f32x4 sacc[2], pacc[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                pacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const int ro = (hh * 32 + t * 16) * D + offr[s];
+                    const u32x4 aq = *reinterpret_cast<const u32x4*>(&s_q[buf][ro]);
+                    const u32x4 ad = *reinterpret_cast<const u32x4*>(&s_do[buf][ro]);
+                    sacc[t] = mfma16x16x32<DT>(aq, kreg[s], sacc[t]);
+                    pacc[t] = mfma16x16x32<DT>(ad, vreg[s], pacc[t]);
+                }
+            }
+            // lane: key jl, rows hh*32 + 16t + 4G + e
+            float p[2][4], ds[2][4];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int ro = hh * 32 + t * 16 + 4 * G;
+                const f32x4 l4 = *reinterpret_cast<const f32x4*>(&s_lse[buf][ro]);
+                const f32x4 d4 = *reinterpret_cast<const f32x4*>(&s_ds[buf][ro]);
+                [[maybe_unused]] f32x4 sl4 = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (BIAS) sl4 = *reinterpret_cast<const f32x4*>(&s_sl[buf][ro]);
+                [[maybe_unused]] int p4[4] = {0, 0, 0, 0};
+                if constexpr (MASK || BIAS) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) p4[e] = s_pos[buf][ro + e];
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float th;
+                    const float x = bw_score<BIAS>(a, sacc[t][e], sl4[e], p4[e] + diag0 - jl, th);
+                    float pv = fast_exp2(x - l4[e]);
+                    if constexpr (MASK) {
+                        const int dg = p4[e] + diag0;
+                        bool vis = p4[e] >= 0 && jl < bb.sk;
+                        if (a.wl >= 0 && jl < dg - a.wl) vis = false;
+                        if (a.wr >= 0 && jl > dg + a.wr) vis = false;
+                        pv = vis ? pv : 0.f;
+                    }
+                    float dsv = pv * (pacc[t][e] - d4[e]) * a.scale;
+                    if constexpr (BIAS) dsv *= 1.f - th * th;
+                    p[t][e] = pv;
+                    ds[t][e] = dsv;
+                }
+            }
+            const u32x4 pk = pack8<DT>(f32x8{p[0][0], p[0][1], p[0][2], p[0][3], p[1][0], p[1][1], p[1][2], p[1][3]});
+            const u32x4 dk = pack8<DT>(f32x8{ds[0][0], ds[0][1], ds[0][2], ds[0][3], ds[1][0], ds[1][1], ds[1][2], ds[1][3]});
+            // dV^T += dO^T . P and dK^T += Q^T . dS (transpose reads of the tiles)
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db) {
+                const int o0 = offt[db] + (32 * hh) * D, o1 = offt[db] + (32 * hh + 16) * D;
+                const u32x2 dl = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_do[buf][o0]));
+                const u32x2 dh = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_do[buf][o1]));
+                const u32x2 ql = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_q[buf][o0]));
+                const u32x2 qh = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_q[buf][o1]));
+                dva[db] = mfma16x16x32<DT>(u32x4{dl[0], dl[1], dh[0], dh[1]}, pk, dva[db]);
+                dka[db] = mfma16x16x32<DT>(u32x4{ql[0], ql[1], qh[0], qh[1]}, dk, dka[db]);
+            }
+        };
+
+        if (ntiles > 0) {
+            load_tile(r_lo);
+            store_tile(0);
+            if (ntiles > 1) load_tile(r_lo + BQ);
+        }
+        __syncthreads();
+        for (int t = 0; t < ntiles; ++t) {
+            const int buf = t & 1;
+            const int rt = r_lo + t * BQ;
+            if (wave_live) {
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int h0 = rt + 32 * hh;  // first packed row of the half
+                    if (h0 >= r_hi) continue;
+                    const int p_lo = h0 / g, p_hi = min(h0 + 31, r_hi - 1) / g;
+                    if (p_hi < wi_lo || p_lo > wi_hi) continue;  // no row of the half sees these keys
+                    bool full = h0 + 32 <= r_hi && jw + 16 <= bb.sk;
+                    if (a.wr >= 0 && jw + 15 > p_lo + diag0 + a.wr) full = false;
+                    if (a.wl >= 0 && jw < p_hi + diag0 - a.wl) full = false;
+                    if (full) half(buf, hh, h0, std::integral_constant<bool, false>{});
+                    else half(buf, hh, h0, std::integral_constant<bool, true>{});
+                }
+            }
+            if (t + 1 < ntiles) store_tile(buf ^ 1);
+            if (t + 2 < ntiles) load_tile(r_lo + (t + 2) * BQ);
+            __syncthreads();
+        }
+
+        // lane holds dK^T / dV^T [dims 16db + 4G + i][key jl]
+        if (wave_live && jl < bb.sk) {
+            uint16_t* dkp = static_cast<uint16_t*>(a.dk) +
+                            (a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.dk_si : (int64_t)b * a.dk_sb) +
+                            (int64_t)jl * a.dk_si + (int64_t)hk * a.dk_sh;
+            uint16_t* dvp = static_cast<uint16_t*>(a.dv) +
+                            (a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.dv_si : (int64_t)b * a.dv_sb) +
+                            (int64_t)jl * a.dv_si + (int64_t)hk * a.dv_sh;
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db) {
+                if (16 * db + 4 * G >= a.hd) continue;
+                uint16_t k4[4] = {f32_to_16<DT>(dka[db][0]), f32_to_16<DT>(dka[db][1]), f32_to_16<DT>(dka[db][2]),
+                                  f32_to_16<DT>(dka[db][3])};
+                uint16_t v4[4] = {f32_to_16<DT>(dva[db][0]), f32_to_16<DT>(dva[db][1]), f32_to_16<DT>(dva[db][2]),
+                                  f32_to_16<DT>(dva[db][3])};
+                *reinterpret_cast<u32x2*>(dkp + 16 * db + 4 * G) = __builtin_bit_cast(u32x2, k4);
+                *reinterpret_cast<u32x2*>(dvp + 16 * db + 4 * G) = __builtin_bit_cast(u32x2, v4);
+            }
+        }
+    }
+}
+
+// ---- dQ -------------------------------------------------------------------------------------
+template <int DT, int HD, bool BIAS>
+__global__ void __launch_bounds__(bw::NT, 1) fa_bwd_dq_kernel(BwdArgs a) {
+    using C = BwCfg<HD>;
+    constexpr int D = C::D, DCH = C::DCH, KSTEPS = C::KSTEPS, DBLK = C::DBLK, RB = C::RB, BM = C::BM, BN = C::BN,
+                  CPK = C::CPK, NT = bw::NT;
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[2][BN * D];  // swz_v: row reads and transpose reads
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[2][BN * D];  // swz_k: row reads
+    __shared__ int s_pref[bw::kMaxBatch + 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, G = lane >> 4;
+    const int total = bw_prefix(a, s_pref, [&](int b) {
+        const BwBatch bb = bw_batch(a, b);
+        return a.Hk * ((bb.rows + BM - 1) / BM);
+    });
+
+    int offkr[KSTEPS], offvr[KSTEPS];
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+        offkr[s] = li * D + (swz_v(li, G * KSTEPS + s) << 3);
+        offvr[s] = li * D + (swz_k(li, G * KSTEPS + s) << 3);
+    }
+    const int r4 = li >> 2, c4 = li & 3;
+    int offt[DBLK];
+#pragma unroll
+    for (int db = 0; db < DBLK; ++db)
+        offt[db] = (4 * G + r4) * D + (swz_v(4 * G + r4, 2 * db + (c4 >> 1)) << 3) + (c4 & 1) * 4;
+    const int dch = tid % DCH, kk0 = tid / DCH;
+
+    const uint16_t* qp = static_cast<const uint16_t*>(a.q);
+    const uint16_t* kp = static_cast<const uint16_t*>(a.k);
+    const uint16_t* vp = static_cast<const uint16_t*>(a.v);
+    const uint16_t* dop = static_cast<const uint16_t*>(a.dout);
+
+    for (int w = blockIdx.x; w < total; w += gridDim.x) {
+        const int b = bw_find_batch(s_pref, a.B, w);
+        const BwBatch bb = bw_batch(a, b);
+        const int local = w - s_pref[b];
+        const int hk = local % a.Hk;
+        const int mt = local / a.Hk;
+        const int g = a.g;
+        const int diag0 = bb.sk - bb.sq;
+        const int tile_row0 = mt * BM;
+        const int tile_rows = min(BM, bb.rows - tile_row0);
+        int k_lo = 0, k_hi = bb.sk;
+        {
+            const int i_lo = tile_row0 / g, i_hi = (tile_row0 + tile_rows - 1) / g;
+            if (a.wl >= 0) k_lo = max(0, i_lo + diag0 - a.wl);
+            if (a.wr >= 0) k_hi = min(bb.sk, i_hi + diag0 + a.wr + 1);
+            if (k_hi < k_lo) k_hi = k_lo;
+        }
+        const int ntiles = (k_hi - k_lo + BN - 1) / BN;
+        const int wrow0 = tile_row0 + wave * RB * 16;
+        const int wrows = min(RB * 16, bb.rows - wrow0);
+        const bool wave_live = wrows > 0;
+        const int wi_lo = wave_live ? wrow0 / g : 0;
+        const int wi_hi = wave_live ? (wrow0 + wrows - 1) / g : 0;
+
+        const int64_t qbase = a.cu_seqlens_q ? (int64_t)a.cu_seqlens_q[b] * a.q_si : (int64_t)b * a.q_sb;
+        const int64_t dobase = a.cu_seqlens_q ? (int64_t)a.cu_seqlens_q[b] * a.do_si : (int64_t)b * a.do_sb;
+        const int64_t kbase = a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.k_si : (int64_t)b * a.k_sb;
+        const int64_t vbase = a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.v_si : (int64_t)b * a.v_sb;
+
+        // q and dout rows as B operands; lse (log2 units) and dsum per row
+        u32x4 qreg[RB][KSTEPS], dreg[RB][KSTEPS];
+        float lse2[RB], dsv[RB], slope[RB];
+        int qi[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const int r = wrow0 + rb * 16 + li;
+            const bool ok = r < bb.rows;
+            const int i = ok ? r / g : 0;
+            const int h = hk * g + (ok ? r % g : 0);
+            qi[rb] = i;
+            const int64_t lo = a.cu_seqlens_q ? (int64_t)h * a.lse_sh + a.cu_seqlens_q[b] + i
+                                              : (int64_t)b * a.lse_sb + (int64_t)h * a.lse_sh + i;
+            lse2[rb] = ok ? a.lse[lo] * kLog2e : INFINITY;
+            dsv[rb] = ok ? a.dsum[lo] : 0.f;
+            slope[rb] = (BIAS && a.alibi && ok) ? a.alibi[(int64_t)b * a.alibi_sb + h] : 0.f;
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) {
+                const int c = G * KSTEPS + s;
+                const bool in = ok && c * 8 < a.hd;
+                qreg[rb][s] = in ? *reinterpret_cast<const u32x4*>(qp + qbase + (int64_t)i * a.q_si + (int64_t)h * a.q_sh + c * 8)
+                                 : u32x4{0u, 0u, 0u, 0u};
+                dreg[rb][s] = in ? *reinterpret_cast<const u32x4*>(dop + dobase + (int64_t)i * a.do_si + (int64_t)h * a.do_sh + c * 8)
+                                 : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): retire the row loads before the tile loop
+
+        f32x4 dqa[RB][DBLK];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db) dqa[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        u32x4 kr[CPK], vr[CPK];
+        auto load_tile = [&](int t0) {
+#pragma unroll
+            for (int u = 0; u < CPK; ++u) {
+                const int j = t0 + kk0 + u * (NT / DCH);
+                if (j < k_hi && dch * 8 < a.hd) {
+                    kr[u] = *reinterpret_cast<const u32x4*>(kp + kbase + (int64_t)j * a.k_si + (int64_t)hk * a.k_sh + dch * 8);
+                    vr[u] = *reinterpret_cast<const u32x4*>(vp + vbase + (int64_t)j * a.v_si + (int64_t)hk * a.v_sh + dch * 8);
+                } else {
+                    kr[u] = u32x4{0u, 0u, 0u, 0u};
+                    vr[u] = u32x4{0u, 0u, 0u, 0u};
+                }
+            }
+        };
+        auto store_tile = [&](int buf) {
+#pragma unroll
+            for (int u = 0; u < CPK; ++u) {
+                const int r = kk0 + u * (NT / DCH);
+                *reinterpret_cast<u32x4*>(&s_k[buf][r * D + (swz_v(r, dch) << 3)]) = kr[u];
+                *reinterpret_cast<u32x4*>(&s_v[buf][r * D + (swz_k(r, dch) << 3)]) = vr[u];
+            }
+        };
+
+        // 32 keys (half hh of the LDS tile) for this wave's rows
+        auto half = [&](int buf, int hh, int s0, auto mask_tag) {
+            constexpr bool MASK = decltype(mask_tag)::value;
+            f32x4 sacc[RB][2], pacc[RB][2];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    sacc[rb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    pacc[rb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    const u32x4 ak = *reinterpret_cast<const u32x4*>(&s_k[buf][offkr[s] + (hh * 32 + kb * 16) * D]);
+                    const u32x4 av = *reinterpret_cast<const u32x4*>(&s_v[buf][offvr[s] + (hh * 32 + kb * 16) * D]);
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb) {
+                        sacc[rb][kb] = mfma16x16x32<DT>(ak, qreg[rb][s], sacc[rb][kb]);
+                        pacc[rb][kb] = mfma16x16x32<DT>(av, dreg[rb][s], pacc[rb][kb]);
+                    }
+                }
+            }
+            // lane: row li of block rb, keys s0 + 16kb + 4G + e
+            u32x4 dsk[RB];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                float ds[2][4];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int j = s0 + kb * 16 + 4 * G + e;
+                        float th;
+                        const float x = bw_score<BIAS>(a, sacc[rb][kb][e], slope[rb], qi[rb] + diag0 - j, th);
+                        float pv = fast_exp2(x - lse2[rb]);
+                        if constexpr (MASK) {
+                            const int dg = qi[rb] + diag0;
+                            bool vis = j < k_hi;
+                            if (a.wl >= 0 && j < dg - a.wl) vis = false;
+                            if (a.wr >= 0 && j > dg + a.wr) vis = false;
+                            pv = vis ? pv : 0.f;
+                        }
+                        float d = pv * (pacc[rb][kb][e] - dsv[rb]) * a.scale;
+                        if constexpr (BIAS) d *= 1.f - th * th;
+                        ds[kb][e] = d;
+                    }
+                dsk[rb] = pack8<DT>(f32x8{ds[0][0], ds[0][1], ds[0][2], ds[0][3], ds[1][0], ds[1][1], ds[1][2], ds[1][3]});
+            }
+            // dQ^T += K^T . dS^T
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db) {
+                const u32x2 l2 = __builtin_bit_cast(
+                    u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_k[buf][offt[db] + (32 * hh) * D]));
+                const u32x2 h2 = __builtin_bit_cast(
+                    u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_k[buf][offt[db] + (32 * hh + 16) * D]));
+                const u32x4 kt = {l2[0], l2[1], h2[0], h2[1]};
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) dqa[rb][db] = mfma16x16x32<DT>(kt, dsk[rb], dqa[rb][db]);
+            }
+        };
+
+        if (ntiles > 0) {
+            load_tile(k_lo);
+            store_tile(0);
+            if (ntiles > 1) load_tile(k_lo + BN);
+        }
+        __syncthreads();
+        for (int t = 0; t < ntiles; ++t) {
+            const int buf = t & 1;
+            const int s0 = k_lo + t * BN, s1 = s0 + BN;
+            bool skip = !wave_live;
+            if (a.wr >= 0 && s0 > wi_hi + diag0 + a.wr) skip = true;
+            if (a.wl >= 0 && s1 - 1 < wi_lo + diag0 - a.wl) skip = true;
+            if (!skip) {
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int h0 = s0 + 32 * hh, h1 = h0 + 32;
+                    bool hskip = h0 >= k_hi;
+                    if (a.wr >= 0 && h0 > wi_hi + diag0 + a.wr) hskip = true;
+                    if (a.wl >= 0 && h1 - 1 < wi_lo + diag0 - a.wl) hskip = true;
+                    if (hskip) continue;
+                    bool full = h1 <= k_hi;
+                    if (a.wl >= 0 && h0 < wi_hi + diag0 - a.wl) full = false;
+                    if (a.wr >= 0 && h1 - 1 > wi_lo + diag0 + a.wr) full = false;
+                    if (full) half(buf, hh, h0, std::integral_constant<bool, false>{});
+                    else half(buf, hh, h0, std::integral_constant<bool, true>{});
+                }
+            }
+            if (t + 1 < ntiles) store_tile(buf ^ 1);
+            if (t + 2 < ntiles) load_tile(k_lo + (t + 2) * BN);
+            __syncthreads();
+        }
+
+        // lane holds dQ^T [dims 16db + 4G + i][row li of block rb]
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const int r = wrow0 + rb * 16 + li;
+            if (r >= bb.rows) continue;
+            const int i = r / g, h = hk * g + r % g;
+            uint16_t* row = static_cast<uint16_t*>(a.dq) +
+                            (a.cu_seqlens_q ? (int64_t)a.cu_seqlens_q[b] * a.dq_si : (int64_t)b * a.dq_sb) +
+                            (int64_t)i * a.dq_si + (int64_t)h * a.dq_sh;
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db) {
+                if (16 * db + 4 * G >= a.hd) continue;
+                uint16_t q4[4] = {f32_to_16<DT>(dqa[rb][db][0]), f32_to_16<DT>(dqa[rb][db][1]),
+                                  f32_to_16<DT>(dqa[rb][db][2]), f32_to_16<DT>(dqa[rb][db][3])};
+                *reinterpret_cast<u32x2*>(row + 16 * db + 4 * G) = __builtin_bit_cast(u32x2, q4);
+            }
+        }
+    }
+}
+
+// ---- host-side launchers (called from fa_api.cpp) -------------------------------------------
+template <int DT, int HD, bool BIAS>
+static void launch_bwd_t(const BwdArgs& a, int grid_kv, int grid_q, hipStream_t stream) {
+    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<DT, HD, BIAS>), dim3(grid_kv), dim3(bw::NT), 0, stream, a);
+    hipLaunchKernelGGL((fa_bwd_dq_kernel<DT, HD, BIAS>), dim3(grid_q), dim3(bw::NT), 0, stream, a);
+}
+
+int bwd_key_block(int d) { return d > 128 ? BwCfg<256>::BK : BwCfg<128>::BK; }
+int bwd_row_block(int d) { return d > 128 ? BwCfg<256>::BM : BwCfg<128>::BM; }
+
+// d: kernel head dim (128); grids: upper bounds on the work items of each kernel
+hipError_t launch_bwd(const BwdArgs& a, int dtype, int d, int grid_kv, int grid_q, hipStream_t stream) {
+    if (d != 128) return hipErrorInvalidValue;
+    const int64_t ntok = a.cu_seqlens_q ? (int64_t)a.total_q : (int64_t)a.B * a.Sq;
+    const int64_t rows = ntok * a.H;
+    if (rows > 0) {
+        const int64_t gsum = (rows + 15) / 16;
+        hipLaunchKernelGGL(fa_bwd_dsum_kernel, dim3((unsigned)gsum), dim3(256), 0, stream, a, dtype);
+    }
+    const bool bias = a.softcap > 0.f || a.alibi != nullptr || !(a.scale > 0.f);
+    if (dtype == DT_BF16) {
+        if (bias) launch_bwd_t<DT_BF16, 128, true>(a, grid_kv, grid_q, stream);
+        else launch_bwd_t<DT_BF16, 128, false>(a, grid_kv, grid_q, stream);
+    } else {
+        if (bias) launch_bwd_t<DT_FP16, 128, true>(a, grid_kv, grid_q, stream);
+        else launch_bwd_t<DT_FP16, 128, false>(a, grid_kv, grid_q, stream);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace fa

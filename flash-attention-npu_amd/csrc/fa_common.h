@@ -62,6 +62,12 @@ __device__ __forceinline__ float f16_to_32(uint16_t h) {
     }
 }
 
+// LDS tile swizzles (16-byte chunk c of row r): swz_k keeps 16 consecutive
+// rows' row reads (one chunk each) on distinct banks; swz_v does the same for
+// the ds_read_b64_tr_b16 transpose reads of 4-row groups.
+__device__ __forceinline__ int swz_k(int r, int c) { return c ^ (r & 15); }
+__device__ __forceinline__ int swz_v(int r, int c) { return c ^ ((r & 3) << 1) ^ (((r >> 2) & 1) << 3); }
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 

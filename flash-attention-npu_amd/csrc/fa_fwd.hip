@@ -200,8 +200,6 @@ struct PfCfg {
     static constexpr int DBLK = D / 16;
 };
 
-__device__ __forceinline__ int swz_k(int r, int c) { return c ^ (r & 15); }
-__device__ __forceinline__ int swz_v(int r, int c) { return c ^ ((r & 3) << 1) ^ (((r >> 2) & 1) << 3); }
 
 // BIAS: softcap, ALiBi or a non-positive scale (scores are formed explicitly);
 // PAGED: K/V rows come through the block table; ROT: q is rotated (kvcache

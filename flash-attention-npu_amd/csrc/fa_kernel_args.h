@@ -69,6 +69,41 @@ struct FwdArgs {
     int rot_dim, rot_interleaved, rot_same_pos, seqlen_ro;
 };
 
+// Backward (dense / varlen). Row layouts as in FwdArgs; lse and dsum share
+// one layout: (B,H,Sq): b*lse_sb + h*lse_sh + i; varlen (H,T): h*lse_sh + cu_q[b] + i.
+struct BwdArgs {
+    const void* q;
+    int64_t q_sb, q_si, q_sh;
+    const void* k;
+    int64_t k_sb, k_si, k_sh;
+    const void* v;
+    int64_t v_sb, v_si, v_sh;
+    const void* out;
+    int64_t o_sb, o_si, o_sh;
+    const void* dout;
+    int64_t do_sb, do_si, do_sh;
+    void* dq;
+    int64_t dq_sb, dq_si, dq_sh;
+    void* dk;
+    int64_t dk_sb, dk_si, dk_sh;
+    void* dv;
+    int64_t dv_sb, dv_si, dv_sh;
+    const float* lse;
+    float* dsum;        // rowsum(dout * out), written by the first kernel
+    int64_t lse_sb, lse_sh;
+    const int* cu_seqlens_q;
+    const int* cu_seqlens_k;
+    const float* alibi;
+    int64_t alibi_sb;
+    float scale;        // softmax_scale
+    float scale_log2;   // softmax_scale * log2(e)
+    float softcap;      // 0 = off
+    int B, Sq, Sk, H, Hk, g;
+    int hd;             // head dim in memory (<= the kernel's)
+    int total_q;        // varlen: rows of q
+    int wl, wr;         // normalised window, -1 = unbounded, causal => wr = 0
+};
+
 struct KvPrepArgs {
     // new tokens (B, S_new, Hk, D) / (B, S_new, Hk, Dv)
     const void* k_new;

@@ -1,6 +1,6 @@
 // fa_torch_ops.cpp -- PyTorch-ROCm operators over the C ABI (libfa_mi355x.so).
 //
-// Registers torch.ops.fa_mi355x.{fwd_kvcache, fwd, varlen_fwd, fwd_combine}.
+// Registers torch.ops.fa_mi355x.{fwd_kvcache, fwd, varlen_fwd, fwd_combine, bwd, varlen_bwd}.
 // Argument order and meaning follow the reference pybind entry points
 // (csrc/arch22/flash_attn_npu_v2/flash_api.cpp: mha_fwd_kvcache :356-377,
 // mha_fwd :628-640, mha_varlen_fwd :828-850, bound at :1301-1309). Unlike the
@@ -371,6 +371,167 @@ std::tuple<Tensor, Tensor> fwd_combine(const Tensor& out_partial, const Tensor& 
     return {out, lse};
 }
 
+// ---- backward (flash_attn_func / flash_attn_varlen_func autograd) ------------------------------
+// The reference binds mha_bwd / mha_varlen_bwd (flash_api.cpp:1063-1299) and
+// returns (dq, dk, dv, softmax_d); so does this op, which allocates dq, dk, dv.
+void set_bwd_common(fa_bwd_params& p, const Tensor& dout, const Tensor& q, const Tensor& k, const Tensor& v,
+                    const Tensor& out, const Tensor& lse) {
+    TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
+    check_dev(k, q, "k");
+    check_dev(v, q, "v");
+    check_dev(out, q, "out");
+    check_dev(dout, q, "dout");
+    check_dev(lse, q, "softmax_lse");
+    p.abi_version = FA_MI355X_ABI_VERSION;
+    p.dtype = dtype_code(q);
+    for (const Tensor* t : {&k, &v, &out, &dout})
+        TORCH_CHECK(t->scalar_type() == q.scalar_type(), "q, k, v, out and dout must have the same dtype");
+    TORCH_CHECK(lse.scalar_type() == at::kFloat, "softmax_lse must be fp32");
+    for (const Tensor* t : {&q, &k, &v, &out, &dout})
+        TORCH_CHECK(t->stride(-1) == 1, "Input tensor must have contiguous last dimension");
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> bwd(const Tensor& dout, const Tensor& q, const Tensor& k, const Tensor& v,
+                                               const Tensor& out, const Tensor& softmax_lse, const OptT& alibi_slopes,
+                                               double p_dropout, double softmax_scale, bool is_causal,
+                                               int64_t window_size_left, int64_t window_size_right, double softcap,
+                                               bool deterministic) {
+    c10::DeviceGuard guard(q.device());
+    fa_bwd_params p{};
+    set_bwd_common(p, dout, q, k, v, out, softmax_lse);
+    TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "q, k, v must have shape (batch, seqlen, heads, head_size)");
+    TORCH_CHECK(dout.sizes() == q.sizes() && out.sizes() == q.sizes(), "out and dout must have the shape of q");
+    TORCH_CHECK(k.sizes() == v.sizes() && k.size(0) == q.size(0) && k.size(3) == q.size(3), "k and v shapes must match q");
+    const int64_t B = q.size(0), Sq = q.size(1), H = q.size(2);
+    TORCH_CHECK(softmax_lse.sizes() == at::IntArrayRef({B, H, Sq}) && softmax_lse.is_contiguous(),
+                "softmax_lse must be a contiguous (batch, nheads, seqlen_q) tensor");
+    Tensor lse = softmax_lse;
+    Tensor dq = at::empty(q.sizes(), q.options());
+    Tensor dk = at::empty(k.sizes(), k.options());
+    Tensor dv = at::empty(v.sizes(), v.options());
+    Tensor sd = at::empty({B, H, Sq}, q.options().dtype(at::kFloat));
+    p.batch = (int32_t)B;
+    p.seqlen_q = (int32_t)Sq;
+    p.seqlen_k = (int32_t)k.size(1);
+    p.nheads = (int32_t)H;
+    p.nheads_k = (int32_t)k.size(2);
+    p.headdim = (int32_t)q.size(3);
+    auto set4 = [](const Tensor& t, const void*& ptr, int64_t& sb, int64_t& si, int64_t& sh) {
+        ptr = t.data_ptr();
+        sb = t.stride(0);
+        si = t.stride(1);
+        sh = t.stride(2);
+    };
+    auto set4m = [](Tensor& t, void*& ptr, int64_t& sb, int64_t& si, int64_t& sh) {
+        ptr = t.data_ptr();
+        sb = t.stride(0);
+        si = t.stride(1);
+        sh = t.stride(2);
+    };
+    set4(q, p.q, p.q_batch_stride, p.q_row_stride, p.q_head_stride);
+    set4(k, p.k, p.k_batch_stride, p.k_row_stride, p.k_head_stride);
+    set4(v, p.v, p.v_batch_stride, p.v_row_stride, p.v_head_stride);
+    set4(out, p.out, p.out_batch_stride, p.out_row_stride, p.out_head_stride);
+    set4(dout, p.dout, p.dout_batch_stride, p.dout_row_stride, p.dout_head_stride);
+    set4m(dq, p.dq, p.dq_batch_stride, p.dq_row_stride, p.dq_head_stride);
+    set4m(dk, p.dk, p.dk_batch_stride, p.dk_row_stride, p.dk_head_stride);
+    set4m(dv, p.dv, p.dv_batch_stride, p.dv_row_stride, p.dv_head_stride);
+    p.softmax_lse = lse.data_ptr<float>();
+    p.softmax_d = sd.data_ptr<float>();
+    if (alibi_slopes.has_value()) {
+        check_dev(*alibi_slopes, q, "alibi_slopes");
+        TORCH_CHECK(alibi_slopes->scalar_type() == at::kFloat && alibi_slopes->stride(-1) == 1,
+                    "ALiBi slopes must be fp32 with a contiguous last dimension");
+        TORCH_CHECK(alibi_slopes->sizes() == at::IntArrayRef({H}) || alibi_slopes->sizes() == at::IntArrayRef({B, H}),
+                    "alibi_slopes must have shape (nheads) or (batch_size, nheads)");
+        p.alibi_slopes = alibi_slopes->data_ptr<float>();
+        p.alibi_batch_stride = alibi_slopes->dim() == 2 ? alibi_slopes->stride(0) : 0;
+    }
+    p.dropout_p = (float)p_dropout;
+    p.softmax_scale = (float)softmax_scale;
+    p.softcap = (float)softcap;
+    p.is_causal = is_causal ? 1 : 0;
+    p.window_size_left = (int32_t)window_size_left;
+    p.window_size_right = (int32_t)window_size_right;
+    p.deterministic = deterministic ? 1 : 0;
+    check_status(fa_mha_bwd(&p, cur_stream()));
+    return {dq, dk, dv, sd};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> varlen_bwd(const Tensor& dout, const Tensor& q, const Tensor& k,
+                                                      const Tensor& v, const Tensor& out, const Tensor& softmax_lse,
+                                                      const Tensor& cu_seqlens_q, const Tensor& cu_seqlens_k,
+                                                      const OptT& alibi_slopes, int64_t max_seqlen_q,
+                                                      int64_t max_seqlen_k, double p_dropout, double softmax_scale,
+                                                      bool is_causal, int64_t window_size_left,
+                                                      int64_t window_size_right, double softcap, bool deterministic) {
+    c10::DeviceGuard guard(q.device());
+    fa_bwd_params p{};
+    set_bwd_common(p, dout, q, k, v, out, softmax_lse);
+    TORCH_CHECK(q.dim() == 3 && k.dim() == 3 && v.dim() == 3, "q, k, v must have shape (total, heads, head_size)");
+    TORCH_CHECK(dout.sizes() == q.sizes() && out.sizes() == q.sizes(), "out and dout must have the shape of q");
+    TORCH_CHECK(k.sizes() == v.sizes() && k.size(2) == q.size(2), "k and v shapes must match q");
+    TORCH_CHECK(cu_seqlens_q.numel() == cu_seqlens_k.numel() && cu_seqlens_q.numel() >= 2,
+                "cu_seqlens_q and cu_seqlens_k must have the same length >= 2");
+    const int64_t T = q.size(0), H = q.size(1);
+    TORCH_CHECK(softmax_lse.sizes() == at::IntArrayRef({H, T}) && softmax_lse.is_contiguous(),
+                "mha_varlen_bwd: softmax_lse must be a contiguous (nheads, total_q) tensor");
+    Tensor dq = at::empty(q.sizes(), q.options());
+    Tensor dk = at::empty(k.sizes(), k.options());
+    Tensor dv = at::empty(v.sizes(), v.options());
+    Tensor sd = at::empty({H, T}, q.options().dtype(at::kFloat));
+    p.batch = (int32_t)(cu_seqlens_q.numel() - 1);
+    p.seqlen_q = (int32_t)max_seqlen_q;
+    p.seqlen_k = (int32_t)max_seqlen_k;
+    p.total_q = (int32_t)T;
+    p.nheads = (int32_t)H;
+    p.nheads_k = (int32_t)k.size(1);
+    p.headdim = (int32_t)q.size(2);
+    auto set3 = [](const Tensor& t, const void*& ptr, int64_t& sb, int64_t& si, int64_t& sh) {
+        ptr = t.data_ptr();
+        sb = 0;
+        si = t.stride(0);
+        sh = t.stride(1);
+    };
+    auto set3m = [](Tensor& t, void*& ptr, int64_t& sb, int64_t& si, int64_t& sh) {
+        ptr = t.data_ptr();
+        sb = 0;
+        si = t.stride(0);
+        sh = t.stride(1);
+    };
+    set3(q, p.q, p.q_batch_stride, p.q_row_stride, p.q_head_stride);
+    set3(k, p.k, p.k_batch_stride, p.k_row_stride, p.k_head_stride);
+    set3(v, p.v, p.v_batch_stride, p.v_row_stride, p.v_head_stride);
+    set3(out, p.out, p.out_batch_stride, p.out_row_stride, p.out_head_stride);
+    set3(dout, p.dout, p.dout_batch_stride, p.dout_row_stride, p.dout_head_stride);
+    set3m(dq, p.dq, p.dq_batch_stride, p.dq_row_stride, p.dq_head_stride);
+    set3m(dk, p.dk, p.dk_batch_stride, p.dk_row_stride, p.dk_head_stride);
+    set3m(dv, p.dv, p.dv_batch_stride, p.dv_row_stride, p.dv_head_stride);
+    p.softmax_lse = softmax_lse.data_ptr<float>();
+    p.softmax_d = sd.data_ptr<float>();
+    p.cu_seqlens_q = i32_ptr(cu_seqlens_q, q, "cu_seqlens_q");
+    p.cu_seqlens_k = i32_ptr(cu_seqlens_k, q, "cu_seqlens_k");
+    if (alibi_slopes.has_value()) {
+        check_dev(*alibi_slopes, q, "alibi_slopes");
+        TORCH_CHECK(alibi_slopes->scalar_type() == at::kFloat && alibi_slopes->stride(-1) == 1,
+                    "ALiBi slopes must be fp32 with a contiguous last dimension");
+        TORCH_CHECK(alibi_slopes->sizes() == at::IntArrayRef({H}) ||
+                        alibi_slopes->sizes() == at::IntArrayRef({(int64_t)p.batch, H}),
+                    "alibi_slopes must have shape (nheads) or (batch_size, nheads)");
+        p.alibi_slopes = alibi_slopes->data_ptr<float>();
+        p.alibi_batch_stride = alibi_slopes->dim() == 2 ? alibi_slopes->stride(0) : 0;
+    }
+    p.dropout_p = (float)p_dropout;
+    p.softmax_scale = (float)softmax_scale;
+    p.softcap = (float)softcap;
+    p.is_causal = is_causal ? 1 : 0;
+    p.window_size_left = (int32_t)window_size_left;
+    p.window_size_right = (int32_t)window_size_right;
+    p.deterministic = deterministic ? 1 : 0;
+    check_status(fa_mha_varlen_bwd(&p, cur_stream()));
+    return {dq, dk, dv, sd};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(fa_mi355x, m) {
@@ -388,6 +549,15 @@ TORCH_LIBRARY(fa_mi355x, m) {
         "Tensor? alibi_slopes, int max_seqlen_q, int max_seqlen_k, float p_dropout, float softmax_scale, "
         "bool is_causal, int window_size_left, int window_size_right, float softcap) -> (Tensor, Tensor)");
     m.def("fwd_combine(Tensor out_partial, Tensor lse_partial, Tensor? out, ScalarType? out_dtype) -> (Tensor, Tensor)");
+    m.def(
+        "bwd(Tensor dout, Tensor q, Tensor k, Tensor v, Tensor out, Tensor softmax_lse, Tensor? alibi_slopes, "
+        "float p_dropout, float softmax_scale, bool is_causal, int window_size_left, int window_size_right, "
+        "float softcap, bool deterministic) -> (Tensor, Tensor, Tensor, Tensor)");
+    m.def(
+        "varlen_bwd(Tensor dout, Tensor q, Tensor k, Tensor v, Tensor out, Tensor softmax_lse, Tensor cu_seqlens_q, "
+        "Tensor cu_seqlens_k, Tensor? alibi_slopes, int max_seqlen_q, int max_seqlen_k, float p_dropout, "
+        "float softmax_scale, bool is_causal, int window_size_left, int window_size_right, float softcap, "
+        "bool deterministic) -> (Tensor, Tensor, Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(fa_mi355x, CUDA, m) {
@@ -395,4 +565,6 @@ TORCH_LIBRARY_IMPL(fa_mi355x, CUDA, m) {
     m.impl("fwd", &fwd);
     m.impl("varlen_fwd", &varlen_fwd);
     m.impl("fwd_combine", &fwd_combine);
+    m.impl("bwd", &bwd);
+    m.impl("varlen_bwd", &varlen_bwd);
 }

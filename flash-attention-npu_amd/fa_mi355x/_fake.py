@@ -33,3 +33,20 @@ def _fwd_combine_fake(out_partial, lse_partial, out, out_dtype):
     dt = out_dtype if out_dtype is not None else torch.float32
     o = out if out is not None else out_partial.new_empty(out_partial.shape[1:], dtype=dt)
     return o, lse_partial.new_empty(lse_partial.shape[1:])
+
+
+@torch.library.register_fake("fa_mi355x::bwd")
+def _bwd_fake(dout, q, k, v, out, softmax_lse, alibi_slopes, p_dropout, softmax_scale, is_causal, window_size_left,
+              window_size_right, softcap, deterministic):
+    b, sq, h, _ = q.shape
+    return (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
+            q.new_empty((b, h, sq), dtype=torch.float32))
+
+
+@torch.library.register_fake("fa_mi355x::varlen_bwd")
+def _varlen_bwd_fake(dout, q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k, alibi_slopes, max_seqlen_q,
+                     max_seqlen_k, p_dropout, softmax_scale, is_causal, window_size_left, window_size_right, softcap,
+                     deterministic):
+    t, h, _ = q.shape
+    return (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
+            q.new_empty((h, t), dtype=torch.float32))

@@ -17,7 +17,8 @@ FA_DTYPE_FP16, FA_DTYPE_BF16, FA_DTYPE_FP32 = 0, 1, 2
 FA_KIND_KVCACHE, FA_KIND_DENSE, FA_KIND_VARLEN = 0, 1, 2
 
 EXPORTED = ["fa_abi_version", "fa_validate", "fa_fwd_workspace_size", "fa_mha_fwd_kvcache", "fa_mha_fwd",
-            "fa_mha_varlen_fwd", "fa_combine", "fa_last_error"]
+            "fa_mha_varlen_fwd", "fa_combine", "fa_last_error", "fa_validate_bwd", "fa_bwd_workspace_size",
+            "fa_mha_bwd", "fa_mha_varlen_bwd"]
 
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
@@ -50,6 +51,28 @@ class FwdParams(ctypes.Structure):
     ]
 
 
+class BwdParams(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", _i32), ("dtype", _i32),
+        ("batch", _i32), ("seqlen_q", _i32), ("seqlen_k", _i32), ("nheads", _i32), ("nheads_k", _i32),
+        ("headdim", _i32), ("total_q", _i32),
+        ("q", _vp), ("q_batch_stride", _i64), ("q_row_stride", _i64), ("q_head_stride", _i64),
+        ("k", _vp), ("k_batch_stride", _i64), ("k_row_stride", _i64), ("k_head_stride", _i64),
+        ("v", _vp), ("v_batch_stride", _i64), ("v_row_stride", _i64), ("v_head_stride", _i64),
+        ("out", _vp), ("out_batch_stride", _i64), ("out_row_stride", _i64), ("out_head_stride", _i64),
+        ("dout", _vp), ("dout_batch_stride", _i64), ("dout_row_stride", _i64), ("dout_head_stride", _i64),
+        ("dq", _vp), ("dq_batch_stride", _i64), ("dq_row_stride", _i64), ("dq_head_stride", _i64),
+        ("dk", _vp), ("dk_batch_stride", _i64), ("dk_row_stride", _i64), ("dk_head_stride", _i64),
+        ("dv", _vp), ("dv_batch_stride", _i64), ("dv_row_stride", _i64), ("dv_head_stride", _i64),
+        ("softmax_lse", _vp), ("softmax_d", _vp),
+        ("cu_seqlens_q", _vp), ("cu_seqlens_k", _vp),
+        ("alibi_slopes", _vp), ("alibi_batch_stride", _i64),
+        ("softmax_scale", ctypes.c_float), ("softcap", ctypes.c_float), ("dropout_p", ctypes.c_float),
+        ("is_causal", _i32), ("window_size_left", _i32), ("window_size_right", _i32), ("deterministic", _i32),
+        ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 _lib = None
 
 
@@ -70,6 +93,14 @@ def lib():
         L.fa_combine.argtypes = [_vp, _vp, _i32, _i64, _i32, _vp, _i64, _i32, _vp, _vp]
         L.fa_combine.restype = ctypes.c_int
         L.fa_last_error.restype = ctypes.c_char_p
+        PB = ctypes.POINTER(BwdParams)
+        L.fa_validate_bwd.argtypes = [PB, _i32]
+        L.fa_validate_bwd.restype = ctypes.c_int
+        L.fa_bwd_workspace_size.argtypes = [PB, _i32, ctypes.POINTER(ctypes.c_size_t)]
+        L.fa_bwd_workspace_size.restype = ctypes.c_int
+        for fn in ("fa_mha_bwd", "fa_mha_varlen_bwd"):
+            getattr(L, fn).argtypes = [PB, _vp]
+            getattr(L, fn).restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -103,3 +134,22 @@ _ENTRY = {FA_KIND_KVCACHE: "fa_mha_fwd_kvcache", FA_KIND_DENSE: "fa_mha_fwd", FA
 
 def forward(p, kind, stream=0):
     return getattr(lib(), _ENTRY[kind])(ctypes.byref(p), stream)
+
+
+def new_bwd_params(**kw):
+    p = BwdParams()
+    p.abi_version = ABI_VERSION
+    p.window_size_left = -1
+    p.window_size_right = -1
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def validate_bwd(p, kind):
+    return lib().fa_validate_bwd(ctypes.byref(p), kind)
+
+
+def backward(p, kind, stream=0):
+    fn = lib().fa_mha_varlen_bwd if kind == FA_KIND_VARLEN else lib().fa_mha_bwd
+    return fn(ctypes.byref(p), stream)

@@ -5,7 +5,10 @@ Function names, keywords, defaults and return arity follow the reference
 flash_attn_varlen_func :1337-1428, flash_attn_with_kvcache :1431-1573, the
 packed variants :965-1336 and the autograd Functions :407-962.
 
-This build implements the forward pass only; calling backward raises.
+The backward of flash_attn_func / flash_attn_varlen_func (and the packed
+variants built on them) runs the MI355X backward kernels
+(interface_arch22.py:204-404,827-857 in the reference); dropout and a paged
+k/v (block_table) have no backward.
 """
 from typing import Optional, Union
 
@@ -50,26 +53,73 @@ def _flash_attn_varlen_forward(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q
     return out, lse, s_dmask, rng_state
 
 
-def _no_backward(*_):
-    raise RuntimeError("flash_attn_npu_v2 on MI355X implements the forward pass only")
+def _flash_attn_backward(dout, q, k, v, out, softmax_lse, dq, dk, dv, dropout_p, softmax_scale, causal,
+                         window_size_left, window_size_right, softcap, alibi_slopes, deterministic, rng_state=None):
+    """Reference interface_arch22.py:204-253: fills dq, dk, dv (when given) and
+    returns softmax_d = rowsum(dout * out), (batch, nheads, seqlen_q) fp32."""
+    dout, q, k, v, out = [maybe_contiguous(x) for x in (dout, q, k, v, out)]
+    gq, gk, gv, softmax_d = ops.bwd(dout, q, k, v, out, softmax_lse.contiguous(), alibi_slopes, float(dropout_p),
+                                    float(softmax_scale), bool(causal), int(window_size_left),
+                                    int(window_size_right), float(softcap), bool(deterministic))
+    for dst, src in ((dq, gq), (dk, gk), (dv, gv)):
+        if dst is not None:
+            dst.copy_(src)
+    return softmax_d if dq is not None else (gq, gk, gv, softmax_d)
+
+
+def _flash_attn_varlen_backward(dout, q, k, v, out, softmax_lse, dq, dk, dv, cu_seqlens_q, cu_seqlens_k,
+                                max_seqlen_q, max_seqlen_k, dropout_p, softmax_scale, causal, window_size_left,
+                                window_size_right, softcap, alibi_slopes, deterministic, rng_state=None,
+                                zero_tensors=False):
+    """Reference interface_arch22.py:296-357."""
+    dout, q, k, v, out = [maybe_contiguous(x) for x in (dout, q, k, v, out)]
+    gq, gk, gv, softmax_d = ops.varlen_bwd(dout, q, k, v, out, softmax_lse.contiguous(), cu_seqlens_q,
+                                           cu_seqlens_k, alibi_slopes, int(max_seqlen_q), int(max_seqlen_k),
+                                           float(dropout_p), float(softmax_scale), bool(causal),
+                                           int(window_size_left), int(window_size_right), float(softcap),
+                                           bool(deterministic))
+    for dst, src in ((dq, gq), (dk, gk), (dv, gv)):
+        if dst is not None:
+            dst.copy_(src)
+    return softmax_d if dq is not None else (gq, gk, gv, softmax_d)
 
 
 class FlashAttnFunc(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, dropout_p, softmax_scale, causal, window_size, softcap, alibi_slopes, deterministic,
                 return_softmax, is_grad_enabled):
+        is_grad = is_grad_enabled and any(x.requires_grad for x in (q, k, v))
         if softmax_scale is None:
             softmax_scale = q.shape[-1] ** (-0.5)
         head_size_og = q.size(3)
         q, k, v = (_pad8(x, head_size_og) for x in (q, k, v))
-        out_padded, softmax_lse, s_dmask, _ = _flash_attn_forward(
+        out_padded, softmax_lse, s_dmask, rng_state = _flash_attn_forward(
             q, k, v, dropout_p, softmax_scale, causal=causal, window_size_left=window_size[0],
             window_size_right=window_size[1], softcap=softcap, alibi_slopes=alibi_slopes,
             return_softmax=return_softmax and dropout_p > 0)
+        if is_grad:
+            ctx.save_for_backward(q, k, v, out_padded, softmax_lse, rng_state)
+            ctx.dropout_p = dropout_p
+            ctx.softmax_scale = softmax_scale
+            ctx.causal = causal
+            ctx.window_size = window_size
+            ctx.softcap = softcap
+            ctx.alibi_slopes = alibi_slopes
+            ctx.deterministic = deterministic
         out = out_padded[..., :head_size_og]
         return out if not return_softmax else (out, softmax_lse, s_dmask)
 
-    backward = staticmethod(_no_backward)
+    @staticmethod
+    def backward(ctx, dout, *args):
+        q, k, v, out, softmax_lse, rng_state = ctx.saved_tensors
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        head_size_og = dout.size(3)
+        dout_padded = _pad8(dout, head_size_og)
+        _flash_attn_backward(dout_padded, q, k, v, out, softmax_lse, dq, dk, dv, ctx.dropout_p, ctx.softmax_scale,
+                             ctx.causal, ctx.window_size[0], ctx.window_size[1], ctx.softcap, ctx.alibi_slopes,
+                             ctx.deterministic, rng_state=rng_state)
+        dq, dk, dv = dq[..., :head_size_og], dk[..., :head_size_og], dv[..., :head_size_og]
+        return dq, dk, dv, None, None, None, None, None, None, None, None, None
 
 
 class FlashAttnVarlenFunc(torch.autograd.Function):
@@ -77,18 +127,43 @@ class FlashAttnVarlenFunc(torch.autograd.Function):
     def forward(ctx, q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p, softmax_scale,
                 causal, window_size, softcap, alibi_slopes, deterministic, return_softmax, block_table,
                 is_grad_enabled):
+        is_grad = is_grad_enabled and any(x.requires_grad for x in (q, k, v))
         if softmax_scale is None:
             softmax_scale = q.shape[-1] ** (-0.5)
         head_size_og = q.size(-1)
         q, k, v = (_pad8(x, head_size_og) for x in (q, k, v))
-        out_padded, softmax_lse, s_dmask, _ = _flash_attn_varlen_forward(
+        out_padded, softmax_lse, s_dmask, rng_state = _flash_attn_varlen_forward(
             q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p, softmax_scale,
             causal=causal, window_size_left=window_size[0], window_size_right=window_size[1], softcap=softcap,
             alibi_slopes=alibi_slopes, return_softmax=return_softmax and dropout_p > 0, block_table=block_table)
+        if is_grad:
+            if block_table is not None:
+                raise RuntimeError("flash_attn_varlen_func has no backward with a paged k/v (block_table)")
+            ctx.save_for_backward(q, k, v, out_padded, softmax_lse, cu_seqlens_q, cu_seqlens_k, rng_state)
+            ctx.dropout_p = dropout_p
+            ctx.max_seqlen_q = max_seqlen_q
+            ctx.max_seqlen_k = max_seqlen_k
+            ctx.softmax_scale = softmax_scale
+            ctx.causal = causal
+            ctx.window_size = window_size
+            ctx.softcap = softcap
+            ctx.alibi_slopes = alibi_slopes
+            ctx.deterministic = deterministic
         out = out_padded[..., :head_size_og]
         return out if not return_softmax else (out, softmax_lse, s_dmask)
 
-    backward = staticmethod(_no_backward)
+    @staticmethod
+    def backward(ctx, dout, *args):
+        q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k, rng_state = ctx.saved_tensors
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        head_size_og = dout.size(2)
+        dout_padded = _pad8(dout, head_size_og)
+        _flash_attn_varlen_backward(dout_padded, q, k, v, out, softmax_lse, dq, dk, dv, cu_seqlens_q, cu_seqlens_k,
+                                    ctx.max_seqlen_q, ctx.max_seqlen_k, ctx.dropout_p, ctx.softmax_scale, ctx.causal,
+                                    ctx.window_size[0], ctx.window_size[1], ctx.softcap, ctx.alibi_slopes,
+                                    ctx.deterministic, rng_state=rng_state)
+        dq, dk, dv = dq[..., :head_size_og], dk[..., :head_size_og], dv[..., :head_size_og]
+        return dq, dk, dv, None, None, None, None, None, None, None, None, None, None, None, None, None, None
 
 
 def flash_attn_qkvpacked_func(qkv, dropout_p=0.0, softmax_scale=None, causal=False, window_size=(-1, -1),

@@ -5,7 +5,9 @@ Names, keywords, defaults and return arity follow the reference
 flash_attn_varlen_func :880-927, flash_attn_combine :930-931,
 flash_attn_with_kvcache :934-1095, get_scheduler_metadata :1098-1138.
 The reference routes all three through one custom op (:63-154); here each
-maps onto the matching fa_mi355x operator. Forward only.
+maps onto the matching fa_mi355x operator. flash_attn_func and
+flash_attn_varlen_func have a backward (the reference's :536-698 autograd
+Functions), run by the MI355X backward kernels.
 """
 from typing import Optional, Union
 
@@ -54,11 +56,22 @@ class FlashAttnFunc(torch.autograd.Function):
         q, k, v = [maybe_contiguous(x) for x in (q, k, v)]
         out, softmax_lse = ops.fwd(q, k, v, None, 0.0, float(softmax_scale), bool(causal), int(window_size[0]),
                                    int(window_size[1]), float(softcap))
+        if any(x.requires_grad for x in (q, k, v)):
+            ctx.save_for_backward(q, k, v, out, softmax_lse)
+            ctx.softmax_scale = softmax_scale
+            ctx.causal = causal
+            ctx.window_size = window_size
+            ctx.softcap = softcap
+            ctx.deterministic = deterministic
         return (out, softmax_lse) if return_softmax else out
 
     @staticmethod
-    def backward(ctx, *args):
-        raise RuntimeError("flash_attn_npu_v3 on MI355X implements the forward pass only")
+    def backward(ctx, dout, *args):
+        q, k, v, out, softmax_lse = ctx.saved_tensors
+        dq, dk, dv, _ = ops.bwd(maybe_contiguous(dout), q, k, v, out, softmax_lse, None, 0.0,
+                                float(ctx.softmax_scale), bool(ctx.causal), int(ctx.window_size[0]),
+                                int(ctx.window_size[1]), float(ctx.softcap), bool(ctx.deterministic))
+        return (dq, dk, dv) + (None,) * 15
 
 
 class FlashAttnVarlenFunc(torch.autograd.Function):
@@ -76,11 +89,28 @@ class FlashAttnVarlenFunc(torch.autograd.Function):
         out, softmax_lse = ops.varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, None, None,
                                           int(max_seqlen_q), int(max_seqlen_k), 0.0, float(softmax_scale),
                                           bool(causal), int(window_size[0]), int(window_size[1]), float(softcap))
+        if any(x.requires_grad for x in (q, k, v)):
+            ctx.save_for_backward(q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k)
+            ctx.has_seqused_k = seqused_k is not None
+            ctx.max_seqlen_q = max_seqlen_q
+            ctx.max_seqlen_k = max_seqlen_k
+            ctx.softmax_scale = softmax_scale
+            ctx.causal = causal
+            ctx.window_size = window_size
+            ctx.softcap = softcap
+            ctx.deterministic = deterministic
         return (out, softmax_lse) if return_softmax else out
 
     @staticmethod
-    def backward(ctx, *args):
-        raise RuntimeError("flash_attn_npu_v3 on MI355X implements the forward pass only")
+    def backward(ctx, dout, *args):
+        if ctx.has_seqused_k:
+            raise RuntimeError("flash_attn_varlen_func has no backward with seqused_k")
+        q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k = ctx.saved_tensors
+        dq, dk, dv, _ = ops.varlen_bwd(maybe_contiguous(dout), q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k,
+                                       None, int(ctx.max_seqlen_q), int(ctx.max_seqlen_k), 0.0,
+                                       float(ctx.softmax_scale), bool(ctx.causal), int(ctx.window_size[0]),
+                                       int(ctx.window_size[1]), float(ctx.softcap), bool(ctx.deterministic))
+        return (dq, dk, dv) + (None,) * 21
 
 
 def flash_attn_func(q, k, v, softmax_scale=None, causal=False, qv=None, q_descale=None, k_descale=None,

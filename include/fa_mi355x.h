@@ -1,9 +1,9 @@
 /*
- * fa_mi355x.h -- C ABI of the MI355X (gfx950) FlashAttention forward library
+ * fa_mi355x.h -- C ABI of the MI355X (gfx950) FlashAttention library
  * (libfa_mi355x.so). Plain pointers, sizes and a stream handle: no torch or
  * HIP types, so any FFI (ctypes, cgo, JNI, N-API) can bind it.
  *
- * The entry points replace the reference's pybind11 forward functions
+ * The entry points replace the reference's pybind11 functions
  * (paths relative to the reference repository):
  *   fa_mha_fwd_kvcache  <- mha_fwd_kvcache  csrc/arch22/flash_attn_npu_v2/flash_api.cpp:356-626
  *                          (bound as fwd_kvcache at flash_api.cpp:1306) and the kvcache branch of
@@ -18,6 +18,11 @@
  *   fa_combine          <- CombineScale (csrc/arch22/flash_attn_npu_v2/CombineScale.hpp:76-357),
  *                          exposed as the v3 flash_attn_combine
  *                          (flash_attn_npu_v3/interface_arch22.py:930-931)
+ *   fa_mha_bwd          <- mha_bwd          csrc/arch22/flash_attn_npu_v2/flash_api.cpp:1251-1299
+ *                          (bound as bwd at flash_api.cpp:1305)
+ *   fa_mha_varlen_bwd   <- mha_varlen_bwd   csrc/arch22/flash_attn_npu_v2/flash_api.cpp:1063-1249
+ *                          (bound as varlen_bwd)
+ *   fa_validate_bwd     <- the host-side checks of those two functions
  *
  * Conventions
  *   - All tensor strides are in ELEMENTS; the last (head) dimension must be
@@ -149,6 +154,71 @@ fa_status_t fa_mha_varlen_fwd(const fa_fwd_params* p, void* stream);
 fa_status_t fa_combine(const float* out_partial, const float* lse_partial, int32_t num_splits, int64_t rows,
                        int32_t headdim_v, void* out, int64_t out_row_stride, int32_t out_dtype, float* lse,
                        void* stream);
+
+/* ---- backward (dense / varlen) ------------------------------------------- */
+typedef struct fa_bwd_params {
+    int32_t abi_version;  /* FA_MI355X_ABI_VERSION */
+    int32_t dtype;        /* fa_dtype_t of q, k, v, out, dout, dq, dk, dv */
+
+    int32_t batch;        /* B */
+    int32_t seqlen_q;     /* Sq (dense), max_seqlen_q (varlen) */
+    int32_t seqlen_k;     /* Sk (dense), max_seqlen_k (varlen) */
+    int32_t nheads;       /* H */
+    int32_t nheads_k;     /* Hk, H % Hk == 0 */
+    int32_t headdim;      /* D: a multiple of 8, at most 128 */
+    int32_t total_q;      /* varlen: rows of q */
+
+    /* q, out, dout, dq: (B, Sq, H, D) or varlen (total_q, H, D);
+       k, v, dk, dv: (B, Sk, Hk, D) or varlen (total_k, Hk, D) */
+    const void* q;
+    int64_t q_batch_stride, q_row_stride, q_head_stride;
+    const void* k;
+    int64_t k_batch_stride, k_row_stride, k_head_stride;
+    const void* v;
+    int64_t v_batch_stride, v_row_stride, v_head_stride;
+    const void* out;
+    int64_t out_batch_stride, out_row_stride, out_head_stride;
+    const void* dout;
+    int64_t dout_batch_stride, dout_row_stride, dout_head_stride;
+    void* dq;
+    int64_t dq_batch_stride, dq_row_stride, dq_head_stride;
+    void* dk;
+    int64_t dk_batch_stride, dk_row_stride, dk_head_stride;
+    void* dv;
+    int64_t dv_batch_stride, dv_row_stride, dv_head_stride;
+
+    /* softmax_lse: the forward's, (B, H, Sq) fp32 or varlen (H, total_q) fp32.
+       softmax_d: output of the same layout, rowsum(dout * out). */
+    const float* softmax_lse;
+    float* softmax_d;
+
+    const int32_t* cu_seqlens_q;    /* varlen: (B+1,) */
+    const int32_t* cu_seqlens_k;    /* varlen: (B+1,) */
+    const float* alibi_slopes;      /* (H,) or (B, H) fp32 */
+    int64_t alibi_batch_stride;     /* 0 for (H,), H for (B, H) */
+
+    float softmax_scale;
+    float softcap;                  /* 0 = off */
+    float dropout_p;                /* must be 0 */
+    int32_t is_causal;
+    int32_t window_size_left;       /* -1 = unbounded */
+    int32_t window_size_right;
+    int32_t deterministic;          /* accepted; the backward is always deterministic */
+
+    void* workspace;                /* unused: fa_bwd_workspace_size reports 0 */
+    size_t workspace_bytes;
+} fa_bwd_params;
+
+/* Host-only validation of a backward call (kind: FA_KIND_DENSE or FA_KIND_VARLEN). */
+fa_status_t fa_validate_bwd(const fa_bwd_params* p, int32_t kind);
+
+/* Bytes of workspace the backward needs (host-only; currently 0). */
+fa_status_t fa_bwd_workspace_size(const fa_bwd_params* p, int32_t kind, size_t* bytes);
+
+/* Backward passes: write dq, dk, dv and softmax_d; enqueue on `stream`.
+ * Deterministic: no atomics, every output element is written by one thread. */
+fa_status_t fa_mha_bwd(const fa_bwd_params* p, void* stream);
+fa_status_t fa_mha_varlen_bwd(const fa_bwd_params* p, void* stream);
 
 /* Thread-local message describing the last non-FA_OK status on this thread. */
 const char* fa_last_error(void);

@@ -42,24 +42,58 @@ def test_library_exports_every_declared_symbol(capi):
     assert capi.lib().fa_abi_version() == capi.ABI_VERSION == 1
 
 
-def test_params_layout_matches_header(capi, tmp_path):
+@pytest.mark.parametrize("struct", ["fa_fwd_params", "fa_bwd_params"])
+def test_params_layout_matches_header(capi, tmp_path, struct):
     """Compile a probe against the header and compare sizeof/offsetof of every
     field with the ctypes mirror."""
-    fields = [n for n, _ in capi.FwdParams._fields_]
+    mirror = {"fa_fwd_params": capi.FwdParams, "fa_bwd_params": capi.BwdParams}[struct]
+    fields = [n for n, _ in mirror._fields_]
     src = tmp_path / "probe.c"
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "fa_mi355x.h"', "int main(void) {",
-             '  printf("size %zu\\n", sizeof(fa_fwd_params));']
+             f'  printf("size %zu\\n", sizeof({struct}));']
     for n in fields:
-        lines.append(f'  printf("{n} %zu\\n", offsetof(fa_fwd_params, {n}));')
+        lines.append(f'  printf("{n} %zu\\n", offsetof({struct}, {n}));')
     lines.append("  return 0; }")
     src.write_text("\n".join(lines))
     exe = tmp_path / "probe"
     subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)], check=True)
     out = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True, check=True)
                .stdout.splitlines())
-    assert int(out["size"]) == ctypes.sizeof(capi.FwdParams)
+    assert int(out["size"]) == ctypes.sizeof(mirror)
     for n in fields:
-        assert int(out[n]) == getattr(capi.FwdParams, n).offset, n
+        assert int(out[n]) == getattr(mirror, n).offset, n
+
+
+def _valid_bwd(capi, **kw):
+    """A dense backward description with fake (aligned, never dereferenced) pointers."""
+    base = dict(dtype=capi.FA_DTYPE_FP16, batch=2, seqlen_q=64, seqlen_k=96, nheads=8, nheads_k=2, headdim=128,
+                softmax_scale=0.088, is_causal=1, softmax_lse=0x90000, softmax_d=0xa0000)
+    for i, n in enumerate(["q", "k", "v", "out", "dout", "dq", "dk", "dv"]):
+        heads = 2 if n in ("k", "v", "dk", "dv") else 8
+        seq = 96 if n in ("k", "v", "dk", "dv") else 64
+        base.update({n: 0x10000 * (i + 1), f"{n}_batch_stride": seq * heads * 128, f"{n}_row_stride": heads * 128,
+                     f"{n}_head_stride": 128})
+    base.update(kw)
+    return capi.new_bwd_params(**base)
+
+
+def test_validate_bwd(capi):
+    assert capi.validate_bwd(_valid_bwd(capi), capi.FA_KIND_DENSE) == capi.FA_OK
+    assert capi.validate_bwd(_valid_bwd(capi, headdim=64), capi.FA_KIND_DENSE) == capi.FA_OK
+    bad = [
+        (dict(dropout_p=0.1), capi.FA_KIND_DENSE, capi.FA_EUNSUPPORTED, "dropout"),
+        (dict(headdim=256), capi.FA_KIND_DENSE, capi.FA_EUNSUPPORTED, "up to 128"),
+        (dict(headdim=264), capi.FA_KIND_DENSE, capi.FA_EINVAL, "at most 256"),
+        (dict(nheads_k=3), capi.FA_KIND_DENSE, capi.FA_EINVAL, "must divide"),
+        (dict(softcap=-1.0), capi.FA_KIND_DENSE, capi.FA_EINVAL, "softcap"),
+        (dict(dq=0x10008), capi.FA_KIND_DENSE, capi.FA_EINVAL, "16-byte aligned"),
+        (dict(softmax_d=None), capi.FA_KIND_DENSE, capi.FA_EINVAL, "softmax_d"),
+        (dict(), capi.FA_KIND_VARLEN, capi.FA_EINVAL, "cu_seqlens_q and cu_seqlens_k are required"),
+        (dict(), capi.FA_KIND_KVCACHE, capi.FA_EINVAL, "dense or varlen"),
+    ]
+    for kw, kind, code, msg in bad:
+        assert capi.validate_bwd(_valid_bwd(capi, **kw), kind) == code, kw
+        assert msg in capi.last_error(), (kw, capi.last_error())
 
 
 def _valid(capi, **kw):
