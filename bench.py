@@ -17,7 +17,10 @@ gets W untimed warmup calls, then untimed calls for about 150 ms more (the
 shader clock ramps up after the idle gap spent building the config's inputs),
 then exactly K timed calls.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c3,c4,c5] [--no-cpu]
+`configs` also carries "bwd", the backward of a dense causal training shape
+(not a BASELINE config).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c3,c4,c5,bwd] [--no-cpu]
 """
 import argparse
 import ctypes
@@ -311,6 +314,54 @@ def cpu_baseline(c, torch):
                       f"{nthreads} OpenMP threads, {reps} reps, {dt * 1e3:.1f} ms/rep"}
 
 
+def bench_bwd(torch, hip, steps, warmup):
+    """Backward of a dense causal training shape through the C ABI
+    (fa_mha_bwd): B=4, S=4096, H=32/8, D=128, bf16. Algorithmic FLOPs follow
+    the usual FlashAttention count, 2.5 x the forward's 4*D per visible
+    (query, key) pair (the five products S, dP, dV, dK, dQ at 2*D each); the
+    kernels' recomputation of S and dP in the dQ pass is not counted."""
+    from fa_mi355x import capi
+    B, S, H, Hk, D = 4, 4096, 32, 8, 128
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    rn = lambda *shape: torch.randn(shape, generator=gen, device="cuda", dtype=torch.float32).to(torch.bfloat16)
+    q, k, v, do = rn(B, S, H, D), rn(B, S, Hk, D), rn(B, S, Hk, D), rn(B, S, H, D)
+    scale = D ** -0.5
+    out, lse = torch.ops.fa_mi355x.fwd(q, k, v, None, 0.0, scale, True, -1, -1, 0.0)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    sd = torch.empty((B, H, S), device="cuda", dtype=torch.float32)
+    kw = dict(dtype=capi.FA_DTYPE_BF16, batch=B, seqlen_q=S, seqlen_k=S, nheads=H, nheads_k=Hk, headdim=D,
+              softmax_lse=lse.data_ptr(), softmax_d=sd.data_ptr(), softmax_scale=scale, is_causal=1)
+    for n, t in (("q", q), ("k", k), ("v", v), ("out", out), ("dout", do), ("dq", dq), ("dk", dk), ("dv", dv)):
+        kw.update({n: t.data_ptr(), f"{n}_batch_stride": t.stride(0), f"{n}_row_stride": t.stride(1),
+                   f"{n}_head_stride": t.stride(2)})
+    p = capi.new_bwd_params(**kw)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def call():
+        if capi.backward(p, capi.FA_KIND_DENSE, stream) != 0:
+            raise RuntimeError(capi.last_error())
+
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < WARM_MS * 1e-3:
+        call()
+        torch.cuda.synchronize()
+    a, b = hip.event(), hip.event()
+    hip.record(a, stream)
+    for _ in range(steps):
+        call()
+    hip.record(b, stream)
+    us = hip.ms(a, b) / steps * 1e3
+    torch.cuda.synchronize()
+    pairs = S * (S + 1) // 2
+    flops = 2.5 * 4 * D * pairs * B * H
+    return {"us_per_call": us, "flops_per_call": flops, "tflops_call": flops / (us * 1e-6) / 1e12,
+            "frac_mfma": flops / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,
+            "workload": f"backward, dense causal B{B} S{S} H{H}/{Hk} D{D} bf16 (dsum + dK/dV + dQ kernels)"}
+
+
 TRAFFIC_PROFILE = "profiles/fa_decode_kernel_hbm_traffic.txt"
 
 
@@ -331,7 +382,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c2,c3,c4,c5")
+    ap.add_argument("--configs", default="c2,c3,c4,c5,bwd")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 plain device copies of 1 GiB (reference for rocprof FETCH_SIZE/WRITE_SIZE)")
@@ -352,6 +403,13 @@ def main():
     results = {}
     cases = {}
     for name in names:
+        if name == "bwd":
+            r = bench_bwd(torch, hip, args.steps, args.warmup)
+            results[name] = r
+            print(f"# {name}: {json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})}",
+                  file=sys.stderr, flush=True)
+            torch.cuda.empty_cache()
+            continue
         ncopy = {"c2": 2, "c3": 2, "c4": 1, "c5": 4}[name]
         c = build_case(name, torch, dev, ncopy)
         torch.cuda.synchronize()
