@@ -445,8 +445,6 @@ fa_status_t validate_bwd(const fa_bwd_params* p, int kind) {
     FA_CHECK(p->nheads % p->nheads_k == 0, "Number of heads in key/value must divide number of heads in query");
     FA_CHECK(p->headdim >= 1 && p->headdim % 8 == 0, "head dimension must be a positive multiple of 8");
     FA_CHECK(p->headdim <= 256, "FlashAttention only supports head dimension at most 256");
-    if (p->headdim > 128)
-        return fail(FA_EUNSUPPORTED, "backward supports head dimensions up to 128 in this build, got %d", p->headdim);
     if (p->dropout_p != 0.f) return fail(FA_EUNSUPPORTED, "dropout is not supported");
     FA_CHECK(p->softcap >= 0.f, "softcap must be non-negative (0.0 disables softcap)");
     FA_CHECK(p->seqlen_q >= 0 && p->seqlen_k >= 0, "sequence lengths must be >= 0");
@@ -544,7 +542,7 @@ fa_status_t run_backward(const fa_bwd_params* p, int kind, void* stream_v) {
     if (p->is_causal) wr = 0;
     a.wl = wl;
     a.wr = wr;
-    const int kd = 128;
+    const int kd = p->headdim <= 128 ? 128 : 256;  // kernel head dim; dims above headdim read as zero
     const int64_t gkv = (int64_t)p->batch * p->nheads_k * ((p->seqlen_k + fa::bwd_key_block(kd) - 1) / fa::bwd_key_block(kd));
     const int64_t gq = (int64_t)p->batch * p->nheads_k *
                        (((int64_t)p->seqlen_q * a.g + fa::bwd_row_block(kd) - 1) / fa::bwd_row_block(kd));

@@ -34,26 +34,33 @@ namespace fa {
 
 namespace bw {
 constexpr int kMaxBatch = 2048;
-constexpr int NW = 8;
-constexpr int NT = NW * 64;
 }  // namespace bw
 
+// Tile shapes per kernel head dim (128 or 256).
 template <int HD>
 struct BwCfg {
     static constexpr int D = HD;
     static constexpr int DCH = D / 8;
     static constexpr int KSTEPS = D / 32;
     static constexpr int DBLK = D / 16;
-    // dK/dV kernel: 16 keys per wave, q tiles of 64 packed rows
-    static constexpr int BK = bw::NW * 16;
+    // dK/dV kernel: 16 keys per wave, q tiles of 64 packed rows. At 256 the
+    // K/V operands and dK^T/dV^T accumulators of a wave take ~200 registers,
+    // so the kernel runs one wave per SIMD (4 waves, MFMA accumulators in the
+    // accumulation registers).
+    static constexpr int KNW = HD > 128 ? 4 : 8;
+    static constexpr int KNT = KNW * 64;
+    static constexpr int BK = KNW * 16;
     static constexpr int BQ = 64;
-    static constexpr int CPQ = BQ * DCH / bw::NT;  // chunks per thread per q (and dout) tile
+    static constexpr int CPQ = BQ * DCH / KNT;  // chunks per thread per q (and dout) tile
     // dQ kernel: 1 row block of 16 per wave (q, dout and dQ^T of two would
-    // not fit 256 VGPRs), key tiles of 64
+    // not fit 256 VGPRs at two waves per SIMD); 8 waves and 64-key tiles at
+    // 128, one wave per SIMD and 32-key tiles at 256
+    static constexpr int QNW = HD > 128 ? 4 : 8;
+    static constexpr int QNT = QNW * 64;
     static constexpr int RB = 1;
-    static constexpr int BM = bw::NW * RB * 16;
-    static constexpr int BN = 64;
-    static constexpr int CPK = BN * DCH / bw::NT;
+    static constexpr int BM = QNW * RB * 16;
+    static constexpr int BN = HD > 128 ? 32 : 64;
+    static constexpr int CPK = BN * DCH / QNT;
 };
 
 struct BwBatch {
@@ -72,10 +79,10 @@ __device__ __forceinline__ BwBatch bw_batch(const BwdArgs& a, int b) {
 
 // Per-batch item prefix in LDS (s_pref[0..B]); items(b) is the work item
 // count of batch b. Every workgroup computes the same table.
-template <class F>
+template <int NT, class F>
 __device__ __forceinline__ int bw_prefix(const BwdArgs& a, int* s_pref, F items) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int b = tid; b < a.B; b += bw::NT) s_pref[b + 1] = items(b);
+    for (int b = tid; b < a.B; b += NT) s_pref[b + 1] = items(b);
     __syncthreads();
     if (wave == 0) {
         const int seg = (a.B + 63) / 64, b0 = lane * seg;
@@ -172,10 +179,10 @@ __global__ void __launch_bounds__(256) fa_bwd_dsum_kernel(BwdArgs a, int dt) {
 
 // ---- dK, dV ---------------------------------------------------------------------------------
 template <int DT, int HD, bool BIAS>
-__global__ void __launch_bounds__(bw::NT, 1) fa_bwd_dkdv_kernel(BwdArgs a) {
+__global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs a) {
     using C = BwCfg<HD>;
     constexpr int D = C::D, DCH = C::DCH, KSTEPS = C::KSTEPS, DBLK = C::DBLK, BK = C::BK, BQ = C::BQ,
-                  CPQ = C::CPQ, NT = bw::NT;
+                  CPQ = C::CPQ, NT = C::KNT;
     __shared__ __attribute__((aligned(16))) uint16_t s_q[2][BQ * D];
     __shared__ __attribute__((aligned(16))) uint16_t s_do[2][BQ * D];
     __shared__ __attribute__((aligned(16))) float s_lse[2][BQ];   // lse * log2(e); +inf for rows past the end
@@ -186,7 +193,7 @@ __global__ void __launch_bounds__(bw::NT, 1) fa_bwd_dkdv_kernel(BwdArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, G = lane >> 4;
-    const int total = bw_prefix(a, s_pref, [&](int b) {
+    const int total = bw_prefix<NT>(a, s_pref, [&](int b) {
         const BwBatch bb = bw_batch(a, b);
         return a.Hk * ((bb.sk + BK - 1) / BK);
     });
@@ -425,17 +432,17 @@ __global__ void __launch_bounds__(bw::NT, 1) fa_bwd_dkdv_kernel(BwdArgs a) {
 
 // ---- dQ -------------------------------------------------------------------------------------
 template <int DT, int HD, bool BIAS>
-__global__ void __launch_bounds__(bw::NT, 1) fa_bwd_dq_kernel(BwdArgs a) {
+__global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a) {
     using C = BwCfg<HD>;
     constexpr int D = C::D, DCH = C::DCH, KSTEPS = C::KSTEPS, DBLK = C::DBLK, RB = C::RB, BM = C::BM, BN = C::BN,
-                  CPK = C::CPK, NT = bw::NT;
+                  CPK = C::CPK, NT = C::QNT;
     __shared__ __attribute__((aligned(16))) uint16_t s_k[2][BN * D];  // swz_v: row reads and transpose reads
     __shared__ __attribute__((aligned(16))) uint16_t s_v[2][BN * D];  // swz_k: row reads
     __shared__ int s_pref[bw::kMaxBatch + 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, G = lane >> 4;
-    const int total = bw_prefix(a, s_pref, [&](int b) {
+    const int total = bw_prefix<NT>(a, s_pref, [&](int b) {
         const BwBatch bb = bw_batch(a, b);
         return a.Hk * ((bb.rows + BM - 1) / BM);
     });
@@ -621,7 +628,7 @@ __global__ void __launch_bounds__(bw::NT, 1) fa_bwd_dq_kernel(BwdArgs a) {
             if (a.wl >= 0 && s1 - 1 < wi_lo + diag0 - a.wl) skip = true;
             if (!skip) {
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
+                for (int hh = 0; hh < BN / 32; ++hh) {
                     const int h0 = s0 + 32 * hh, h1 = h0 + 32;
                     bool hskip = h0 >= k_hi;
                     if (a.wr >= 0 && h0 > wi_hi + diag0 + a.wr) hskip = true;
@@ -662,30 +669,36 @@ __global__ void __launch_bounds__(bw::NT, 1) fa_bwd_dq_kernel(BwdArgs a) {
 // ---- host-side launchers (called from fa_api.cpp) -------------------------------------------
 template <int DT, int HD, bool BIAS>
 static void launch_bwd_t(const BwdArgs& a, int grid_kv, int grid_q, hipStream_t stream) {
-    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<DT, HD, BIAS>), dim3(grid_kv), dim3(bw::NT), 0, stream, a);
-    hipLaunchKernelGGL((fa_bwd_dq_kernel<DT, HD, BIAS>), dim3(grid_q), dim3(bw::NT), 0, stream, a);
+    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<DT, HD, BIAS>), dim3(grid_kv), dim3(BwCfg<HD>::KNT), 0, stream, a);
+    hipLaunchKernelGGL((fa_bwd_dq_kernel<DT, HD, BIAS>), dim3(grid_q), dim3(BwCfg<HD>::QNT), 0, stream, a);
+}
+
+template <int HD>
+static void launch_bwd_d(const BwdArgs& a, int dtype, int grid_kv, int grid_q, hipStream_t stream) {
+    const bool bias = a.softcap > 0.f || a.alibi != nullptr || !(a.scale > 0.f);
+    if (dtype == DT_BF16) {
+        if (bias) launch_bwd_t<DT_BF16, HD, true>(a, grid_kv, grid_q, stream);
+        else launch_bwd_t<DT_BF16, HD, false>(a, grid_kv, grid_q, stream);
+    } else {
+        if (bias) launch_bwd_t<DT_FP16, HD, true>(a, grid_kv, grid_q, stream);
+        else launch_bwd_t<DT_FP16, HD, false>(a, grid_kv, grid_q, stream);
+    }
 }
 
 int bwd_key_block(int d) { return d > 128 ? BwCfg<256>::BK : BwCfg<128>::BK; }
 int bwd_row_block(int d) { return d > 128 ? BwCfg<256>::BM : BwCfg<128>::BM; }
 
-// d: kernel head dim (128); grids: upper bounds on the work items of each kernel
+// d: kernel head dim (128 or 256); grids: upper bounds on the work items of each kernel
 hipError_t launch_bwd(const BwdArgs& a, int dtype, int d, int grid_kv, int grid_q, hipStream_t stream) {
-    if (d != 128) return hipErrorInvalidValue;
+    if (d != 128 && d != 256) return hipErrorInvalidValue;
     const int64_t ntok = a.cu_seqlens_q ? (int64_t)a.total_q : (int64_t)a.B * a.Sq;
     const int64_t rows = ntok * a.H;
     if (rows > 0) {
         const int64_t gsum = (rows + 15) / 16;
         hipLaunchKernelGGL(fa_bwd_dsum_kernel, dim3((unsigned)gsum), dim3(256), 0, stream, a, dtype);
     }
-    const bool bias = a.softcap > 0.f || a.alibi != nullptr || !(a.scale > 0.f);
-    if (dtype == DT_BF16) {
-        if (bias) launch_bwd_t<DT_BF16, 128, true>(a, grid_kv, grid_q, stream);
-        else launch_bwd_t<DT_BF16, 128, false>(a, grid_kv, grid_q, stream);
-    } else {
-        if (bias) launch_bwd_t<DT_FP16, 128, true>(a, grid_kv, grid_q, stream);
-        else launch_bwd_t<DT_FP16, 128, false>(a, grid_kv, grid_q, stream);
-    }
+    if (d == 128) launch_bwd_d<128>(a, dtype, grid_kv, grid_q, stream);
+    else launch_bwd_d<256>(a, dtype, grid_kv, grid_q, stream);
     return hipGetLastError();
 }
 

@@ -165,7 +165,7 @@ typedef struct fa_bwd_params {
     int32_t seqlen_k;     /* Sk (dense), max_seqlen_k (varlen) */
     int32_t nheads;       /* H */
     int32_t nheads_k;     /* Hk, H % Hk == 0 */
-    int32_t headdim;      /* D: a multiple of 8, at most 128 */
+    int32_t headdim;      /* D: a multiple of 8, at most 256 */
     int32_t total_q;      /* varlen: rows of q */
 
     /* q, out, dout, dq: (B, Sq, H, D) or varlen (total_q, H, D);

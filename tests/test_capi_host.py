@@ -79,10 +79,10 @@ def _valid_bwd(capi, **kw):
 
 def test_validate_bwd(capi):
     assert capi.validate_bwd(_valid_bwd(capi), capi.FA_KIND_DENSE) == capi.FA_OK
-    assert capi.validate_bwd(_valid_bwd(capi, headdim=64), capi.FA_KIND_DENSE) == capi.FA_OK
+    for d in (64, 136, 192, 256):
+        assert capi.validate_bwd(_valid_bwd(capi, headdim=d), capi.FA_KIND_DENSE) == capi.FA_OK, d
     bad = [
         (dict(dropout_p=0.1), capi.FA_KIND_DENSE, capi.FA_EUNSUPPORTED, "dropout"),
-        (dict(headdim=256), capi.FA_KIND_DENSE, capi.FA_EUNSUPPORTED, "up to 128"),
         (dict(headdim=264), capi.FA_KIND_DENSE, capi.FA_EINVAL, "at most 256"),
         (dict(nheads_k=3), capi.FA_KIND_DENSE, capi.FA_EINVAL, "must divide"),
         (dict(softcap=-1.0), capi.FA_KIND_DENSE, capi.FA_EINVAL, "softcap"),

@@ -162,6 +162,26 @@ def test_bwd_varlen_window(case):
     run_varlen(dtype, H, Hk, lq, lk, D, causal, window=(wl, wr), softcap=softcap, seed=wl + 3 * wr + D)
 
 
+# head dims above 128 (reference test_cases_varlen :225-226,231-232 use 192 and 256)
+@pytest.mark.parametrize("case", [
+    (torch.float16, 5, 1, [777], [888], 192, False, 0.0),
+    (torch.float16, 5, 1, [777], [1000], 256, True, 0.0),
+    (torch.float16, 5, 1, [777], [888], 192, False, 30.0),
+    (torch.bfloat16, 4, 2, [300, 1, 129], [300, 64, 500], 256, True, 30.0),
+], ids=["d192", "d256", "d192_softcap", "d256_ragged_softcap"])
+def test_bwd_varlen_large_headdim(case):
+    dtype, H, Hk, lq, lk, D, causal, softcap = case
+    run_varlen(dtype, H, Hk, lq, lk, D, causal, softcap=softcap, seed=D + len(lq))
+
+
+def test_bwd_dense_headdim_256_window_gqa():
+    run_dense(torch.bfloat16, 2, 8, 2, 300, 333, 256, True, window=(100, 0), seed=17)
+
+
+def test_bwd_dense_headdim_136():
+    run_dense(torch.float16, 2, 4, 4, 200, 200, 136, False, seed=18)
+
+
 def test_bwd_alibi():
     # ALiBi gradients (the reference's backward ignores alibi_slopes; here the
     # bias enters as in the forward)
