@@ -47,9 +47,14 @@ struct BwCfg {
     // K/V operands and dK^T/dV^T accumulators of a wave take ~200 registers,
     // so the kernel runs one wave per SIMD (4 waves, MFMA accumulators in the
     // accumulation registers).
-    static constexpr int KNW = HD > 128 ? 4 : 8;
+#ifndef BW_KRB
+#define BW_KRB 1
+#define BW_KNW 8
+#endif
+    static constexpr int KNW = HD > 128 ? 4 : BW_KNW;
+    static constexpr int KRB = HD > 128 ? 1 : BW_KRB;  // 16-key blocks per wave
     static constexpr int KNT = KNW * 64;
-    static constexpr int BK = KNW * 16;
+    static constexpr int BK = KNW * 16 * KRB;
     static constexpr int BQ = 64;
     static constexpr int CPQ = BQ * DCH / KNT;  // chunks per thread per q (and dout) tile
     // dQ kernel: 1 row block of 16 per wave (q, dout and dQ^T of two would
@@ -182,7 +187,7 @@ template <int DT, int HD, bool BIAS>
 __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs a) {
     using C = BwCfg<HD>;
     constexpr int D = C::D, DCH = C::DCH, KSTEPS = C::KSTEPS, DBLK = C::DBLK, BK = C::BK, BQ = C::BQ,
-                  CPQ = C::CPQ, NT = C::KNT;
+                  CPQ = C::CPQ, NT = C::KNT, KRB = C::KRB;
     __shared__ __attribute__((aligned(16))) uint16_t s_q[2][BQ * D];
     __shared__ __attribute__((aligned(16))) uint16_t s_do[2][BQ * D];
     __shared__ __attribute__((aligned(16))) float s_lse[2][BQ];   // lse * log2(e); +inf for rows past the end
@@ -229,18 +234,22 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
         const int64_t kbase = a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.k_si : (int64_t)b * a.k_sb;
         const int64_t vbase = a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.v_si : (int64_t)b * a.v_sb;
 
-        // this wave's 16 keys as B operands: lane holds key (j0 + 16*wave + li), chunk G*KSTEPS + s
-        const int jw = j0 + 16 * wave;
-        const int jl = jw + li;
-        u32x4 kreg[KSTEPS], vreg[KSTEPS];
+        // this wave's KRB blocks of 16 keys as B operands: block rk, lane holds
+        // key (jw + 16*rk + li), chunk G*KSTEPS + s
+        const int jw = j0 + 16 * KRB * wave;
+        u32x4 kreg[KRB][KSTEPS], vreg[KRB][KSTEPS];
 #pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) {
-            const int c = G * KSTEPS + s;
-            const bool in = jl < bb.sk && c * 8 < a.hd;
-            kreg[s] = in ? *reinterpret_cast<const u32x4*>(kp + kbase + (int64_t)jl * a.k_si + (int64_t)hk * a.k_sh + c * 8)
-                         : u32x4{0u, 0u, 0u, 0u};
-            vreg[s] = in ? *reinterpret_cast<const u32x4*>(vp + vbase + (int64_t)jl * a.v_si + (int64_t)hk * a.v_sh + c * 8)
-                         : u32x4{0u, 0u, 0u, 0u};
+        for (int rk = 0; rk < KRB; ++rk) {
+            const int jl = jw + 16 * rk + li;
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) {
+                const int c = G * KSTEPS + s;
+                const bool in = jl < bb.sk && c * 8 < a.hd;
+                kreg[rk][s] = in ? *reinterpret_cast<const u32x4*>(kp + kbase + (int64_t)jl * a.k_si + (int64_t)hk * a.k_sh + c * 8)
+                                 : u32x4{0u, 0u, 0u, 0u};
+                vreg[rk][s] = in ? *reinterpret_cast<const u32x4*>(vp + vbase + (int64_t)jl * a.v_si + (int64_t)hk * a.v_sh + c * 8)
+                                 : u32x4{0u, 0u, 0u, 0u};
+            }
         }
 
         // packed rows that can see any key of [j0, j0 + BK)
@@ -250,18 +259,21 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
         const int r_lo = i_lo * g;
         const int r_hi = (i_hi >= i_lo) ? (i_hi + 1) * g : r_lo;
         const int ntiles = (r_hi - r_lo + BQ - 1) / BQ;
-        // the same range for this wave's 16 keys (skips tiles it cannot see)
+        // the same range for this wave's keys (skips tiles it cannot see)
+        constexpr int WK = 16 * KRB;
         int wi_lo = 0, wi_hi = bb.sq - 1;
         if (a.wr >= 0) wi_lo = max(0, jw - diag0 - a.wr);
-        if (a.wl >= 0) wi_hi = min(bb.sq - 1, jw + 15 - diag0 + a.wl);
+        if (a.wl >= 0) wi_hi = min(bb.sq - 1, jw + WK - 1 - diag0 + a.wl);
         const bool wave_live = jw < bb.sk;
 
-        f32x4 dka[DBLK], dva[DBLK];
+        f32x4 dka[KRB][DBLK], dva[KRB][DBLK];
 #pragma unroll
-        for (int db = 0; db < DBLK; ++db) {
-            dka[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-            dva[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
+        for (int rk = 0; rk < KRB; ++rk)
+#pragma unroll
+            for (int db = 0; db < DBLK; ++db) {
+                dka[rk][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+                dva[rk][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
 
         u32x4 qr[CPQ], dr[CPQ];
         float lr = 0.f, dsr = 0.f, slr = 0.f;
@@ -313,15 +325,17 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
             }
         };
 
-        // 32 rows (half tile hh) against this wave's 16 keys
-        auto half = [&](int buf, int hh, int rbase, auto mask_tag) {
+        // 32 rows (half tile hh) against this wave's keys
+        auto half = [&](int buf, int hh, auto mask_tag) {
             constexpr bool MASK = decltype(mask_tag)::value;
-            f32x4 sacc[2], pacc[2];
+            f32x4 sacc[KRB][2], pacc[KRB][2];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                sacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-                pacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
+            for (int rk = 0; rk < KRB; ++rk)
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    sacc[rk][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    pacc[rk][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s) {
 #pragma unroll
@@ -329,45 +343,57 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
                     const int ro = (hh * 32 + t * 16) * D + offr[s];
                     const u32x4 aq = *reinterpret_cast<const u32x4*>(&s_q[buf][ro]);
                     const u32x4 ad = *reinterpret_cast<const u32x4*>(&s_do[buf][ro]);
-                    sacc[t] = mfma16x16x32<DT>(aq, kreg[s], sacc[t]);
-                    pacc[t] = mfma16x16x32<DT>(ad, vreg[s], pacc[t]);
+#pragma unroll
+                    for (int rk = 0; rk < KRB; ++rk) {
+                        sacc[rk][t] = mfma16x16x32<DT>(aq, kreg[rk][s], sacc[rk][t]);
+                        pacc[rk][t] = mfma16x16x32<DT>(ad, vreg[rk][s], pacc[rk][t]);
+                    }
                 }
             }
-            // lane: key jl, rows hh*32 + 16t + 4G + e
-            float p[2][4], ds[2][4];
+            // lane: key jw + 16rk + li, rows hh*32 + 16t + 4G + e
+            f32x4 l4[2], d4[2];
+            [[maybe_unused]] f32x4 sl4[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+            [[maybe_unused]] int p4[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int ro = hh * 32 + t * 16 + 4 * G;
-                const f32x4 l4 = *reinterpret_cast<const f32x4*>(&s_lse[buf][ro]);
-                const f32x4 d4 = *reinterpret_cast<const f32x4*>(&s_ds[buf][ro]);
-                [[maybe_unused]] f32x4 sl4 = {0.f, 0.f, 0.f, 0.f};
-                if constexpr (BIAS) sl4 = *reinterpret_cast<const f32x4*>(&s_sl[buf][ro]);
-                [[maybe_unused]] int p4[4] = {0, 0, 0, 0};
+                l4[t] = *reinterpret_cast<const f32x4*>(&s_lse[buf][ro]);
+                d4[t] = *reinterpret_cast<const f32x4*>(&s_ds[buf][ro]);
+                if constexpr (BIAS) sl4[t] = *reinterpret_cast<const f32x4*>(&s_sl[buf][ro]);
                 if constexpr (MASK || BIAS) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) p4[e] = s_pos[buf][ro + e];
-                }
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float th;
-                    const float x = bw_score<BIAS>(a, sacc[t][e], sl4[e], p4[e] + diag0 - jl, th);
-                    float pv = fast_exp2(x - l4[e]);
-                    if constexpr (MASK) {
-                        const int dg = p4[e] + diag0;
-                        bool vis = p4[e] >= 0 && jl < bb.sk;
-                        if (a.wl >= 0 && jl < dg - a.wl) vis = false;
-                        if (a.wr >= 0 && jl > dg + a.wr) vis = false;
-                        pv = vis ? pv : 0.f;
-                    }
-                    float dsv = pv * (pacc[t][e] - d4[e]) * a.scale;
-                    if constexpr (BIAS) dsv *= 1.f - th * th;
-                    p[t][e] = pv;
-                    ds[t][e] = dsv;
+                    for (int e = 0; e < 4; ++e) p4[t][e] = s_pos[buf][ro + e];
                 }
             }
-            const u32x4 pk = pack8<DT>(f32x8{p[0][0], p[0][1], p[0][2], p[0][3], p[1][0], p[1][1], p[1][2], p[1][3]});
-            const u32x4 dk = pack8<DT>(f32x8{ds[0][0], ds[0][1], ds[0][2], ds[0][3], ds[1][0], ds[1][1], ds[1][2], ds[1][3]});
-            // dV^T += dO^T . P and dK^T += Q^T . dS (transpose reads of the tiles)
+            u32x4 pk[KRB], dk[KRB];
+#pragma unroll
+            for (int rk = 0; rk < KRB; ++rk) {
+                const int jl = jw + 16 * rk + li;
+                float p[2][4], ds[2][4];
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float th;
+                        const float x = bw_score<BIAS>(a, sacc[rk][t][e], sl4[t][e], p4[t][e] + diag0 - jl, th);
+                        float pv = fast_exp2(x - l4[t][e]);
+                        if constexpr (MASK) {
+                            const int dg = p4[t][e] + diag0;
+                            bool vis = p4[t][e] >= 0 && jl < bb.sk;
+                            if (a.wl >= 0 && jl < dg - a.wl) vis = false;
+                            if (a.wr >= 0 && jl > dg + a.wr) vis = false;
+                            pv = vis ? pv : 0.f;
+                        }
+                        float dsv = pv * (pacc[rk][t][e] - d4[t][e]) * a.scale;
+                        if constexpr (BIAS) dsv *= 1.f - th * th;
+                        p[t][e] = pv;
+                        ds[t][e] = dsv;
+                    }
+                pk[rk] = pack8<DT>(f32x8{p[0][0], p[0][1], p[0][2], p[0][3], p[1][0], p[1][1], p[1][2], p[1][3]});
+                dk[rk] = pack8<DT>(f32x8{ds[0][0], ds[0][1], ds[0][2], ds[0][3], ds[1][0], ds[1][1], ds[1][2], ds[1][3]});
+            }
+            // dV^T += dO^T . P and dK^T += Q^T . dS (transpose reads of the
+            // tiles, shared by the wave's key blocks)
 #pragma unroll
             for (int db = 0; db < DBLK; ++db) {
                 const int o0 = offt[db] + (32 * hh) * D, o1 = offt[db] + (32 * hh + 16) * D;
@@ -375,8 +401,12 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
                 const u32x2 dh = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_do[buf][o1]));
                 const u32x2 ql = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_q[buf][o0]));
                 const u32x2 qh = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_q[buf][o1]));
-                dva[db] = mfma16x16x32<DT>(u32x4{dl[0], dl[1], dh[0], dh[1]}, pk, dva[db]);
-                dka[db] = mfma16x16x32<DT>(u32x4{ql[0], ql[1], qh[0], qh[1]}, dk, dka[db]);
+                const u32x4 dot = {dl[0], dl[1], dh[0], dh[1]}, qt = {ql[0], ql[1], qh[0], qh[1]};
+#pragma unroll
+                for (int rk = 0; rk < KRB; ++rk) {
+                    dva[rk][db] = mfma16x16x32<DT>(dot, pk[rk], dva[rk][db]);
+                    dka[rk][db] = mfma16x16x32<DT>(qt, dk[rk], dka[rk][db]);
+                }
             }
         };
 
@@ -396,11 +426,11 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
                     if (h0 >= r_hi) continue;
                     const int p_lo = h0 / g, p_hi = min(h0 + 31, r_hi - 1) / g;
                     if (p_hi < wi_lo || p_lo > wi_hi) continue;  // no row of the half sees these keys
-                    bool full = h0 + 32 <= r_hi && jw + 16 <= bb.sk;
-                    if (a.wr >= 0 && jw + 15 > p_lo + diag0 + a.wr) full = false;
+                    bool full = h0 + 32 <= r_hi && jw + WK <= bb.sk;
+                    if (a.wr >= 0 && jw + WK - 1 > p_lo + diag0 + a.wr) full = false;
                     if (a.wl >= 0 && jw < p_hi + diag0 - a.wl) full = false;
-                    if (full) half(buf, hh, h0, std::integral_constant<bool, false>{});
-                    else half(buf, hh, h0, std::integral_constant<bool, true>{});
+                    if (full) half(buf, hh, std::integral_constant<bool, false>{});
+                    else half(buf, hh, std::integral_constant<bool, true>{});
                 }
             }
             if (t + 1 < ntiles) store_tile(buf ^ 1);
@@ -408,23 +438,28 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
             __syncthreads();
         }
 
-        // lane holds dK^T / dV^T [dims 16db + 4G + i][key jl]
-        if (wave_live && jl < bb.sk) {
-            uint16_t* dkp = static_cast<uint16_t*>(a.dk) +
-                            (a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.dk_si : (int64_t)b * a.dk_sb) +
-                            (int64_t)jl * a.dk_si + (int64_t)hk * a.dk_sh;
-            uint16_t* dvp = static_cast<uint16_t*>(a.dv) +
-                            (a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.dv_si : (int64_t)b * a.dv_sb) +
-                            (int64_t)jl * a.dv_si + (int64_t)hk * a.dv_sh;
+        // lane holds dK^T / dV^T [dims 16db + 4G + i][key jw + 16rk + li]
+        if (wave_live) {
 #pragma unroll
-            for (int db = 0; db < DBLK; ++db) {
-                if (16 * db + 4 * G >= a.hd) continue;
-                uint16_t k4[4] = {f32_to_16<DT>(dka[db][0]), f32_to_16<DT>(dka[db][1]), f32_to_16<DT>(dka[db][2]),
-                                  f32_to_16<DT>(dka[db][3])};
-                uint16_t v4[4] = {f32_to_16<DT>(dva[db][0]), f32_to_16<DT>(dva[db][1]), f32_to_16<DT>(dva[db][2]),
-                                  f32_to_16<DT>(dva[db][3])};
-                *reinterpret_cast<u32x2*>(dkp + 16 * db + 4 * G) = __builtin_bit_cast(u32x2, k4);
-                *reinterpret_cast<u32x2*>(dvp + 16 * db + 4 * G) = __builtin_bit_cast(u32x2, v4);
+            for (int rk = 0; rk < KRB; ++rk) {
+                const int jl = jw + 16 * rk + li;
+                if (jl >= bb.sk) continue;
+                uint16_t* dkp = static_cast<uint16_t*>(a.dk) +
+                                (a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.dk_si : (int64_t)b * a.dk_sb) +
+                                (int64_t)jl * a.dk_si + (int64_t)hk * a.dk_sh;
+                uint16_t* dvp = static_cast<uint16_t*>(a.dv) +
+                                (a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.dv_si : (int64_t)b * a.dv_sb) +
+                                (int64_t)jl * a.dv_si + (int64_t)hk * a.dv_sh;
+#pragma unroll
+                for (int db = 0; db < DBLK; ++db) {
+                    if (16 * db + 4 * G >= a.hd) continue;
+                    uint16_t k4[4] = {f32_to_16<DT>(dka[rk][db][0]), f32_to_16<DT>(dka[rk][db][1]),
+                                      f32_to_16<DT>(dka[rk][db][2]), f32_to_16<DT>(dka[rk][db][3])};
+                    uint16_t v4[4] = {f32_to_16<DT>(dva[rk][db][0]), f32_to_16<DT>(dva[rk][db][1]),
+                                      f32_to_16<DT>(dva[rk][db][2]), f32_to_16<DT>(dva[rk][db][3])};
+                    *reinterpret_cast<u32x2*>(dkp + 16 * db + 4 * G) = __builtin_bit_cast(u32x2, k4);
+                    *reinterpret_cast<u32x2*>(dvp + 16 * db + 4 * G) = __builtin_bit_cast(u32x2, v4);
+                }
             }
         }
     }

@@ -435,21 +435,26 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     end_seg(cs);
 }
 
-// Merge of the partials a segment left in the decode kernel (one workgroup
-// per segment; a segment with no visible key gets out = 0, lse = +inf): per
-// row, lse = M + ln(sum_j exp(lse_j - M)) and O = sum_j exp(lse_j - lse) * O_j
-// (the closed form of CombineScale.hpp:150-194). The partial list of a
-// segment [S, S+n) is known from the worker split alone: workers
-// owner(S)..owner(S+n-1) when every worker has a tile (T >= W), else one
-// worker per tile. Phase 1 reduces max / sum of the partial LSEs over
-// threads; phase 2 spreads the independent partial-O loads over NG groups of
-// threads and reduces the groups in LDS, so no load waits on another.
+// Merge of the partials a segment left in the decode kernel (4 workgroups per
+// segment, one per quarter of the head dim; a segment with no visible key
+// gets out = 0, lse = +inf): per row, lse = M + ln(sum_j exp(lse_j - M)) and
+// O = sum_j exp(lse_j - lse) * O_j (the closed form of
+// CombineScale.hpp:150-194). The partial list of a segment [S, S+n) is known
+// from the worker split alone: workers owner(S)..owner(S+n-1) when every
+// worker has a tile (T >= W), else one worker per tile. NG thread groups each
+// fold a share of the partials in one pass with a running maximum (the lse
+// and O of a partial are loaded together), and the groups are combined in
+// LDS. (Merging inside the decode kernel, by the last wave to finish a
+// segment, was measured 1.6x slower: every partial then needs a device-scope
+// fence, i.e. an L2 write-back across the 8 XCDs.)
 template <int DT>
 __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int workers) {
     using namespace dec;
-    __shared__ float s_m[16][17], s_s[16][17];
     __shared__ __attribute__((aligned(16))) float s_acc[256][8];
-    const int sig = blockIdx.x;
+    __shared__ float s_gm[256], s_gs[256];
+    constexpr int DSPLIT = 4;            // workgroups per segment, each merging D / DSPLIT dims
+    constexpr int CH = D / DSPLIT / 8;   // 8-dim chunks per row in one workgroup
+    const int sig = blockIdx.x / DSPLIT, dsl = blockIdx.x % DSPLIT;
     const int b = sig / a.Hk, hk = sig % a.Hk;
     if (b >= a.B) return;
     int sq = a.cu_seqlens_q ? a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b] : a.Sq;
@@ -475,68 +480,63 @@ __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int wor
         const int slot = (j == 0 && w * T / W < S) ? 1 : 0;
         return (w * 2 + slot) * 16;
     };
-    // ---- phase 1: per-row max and sum over the partial LSEs -----------------------
-    {
-        const int rr = tid & 15, js = tid >> 4;
-        float m = -INFINITY, sum = 0.f;
-        if (rr < rows) {
-            for (int j = js; j < n; j += 16) {
-                const float v = a.part_lse[prow0(j) + rr];
-                if (v != -INFINITY) {
-                    const float mn = fmaxf(m, v);
-                    sum = sum * fast_exp2((m - mn) * kLog2e) + fast_exp2((v - mn) * kLog2e);
-                    m = mn;
-                }
-            }
-        }
-        s_m[rr][js] = m;
-        s_s[rr][js] = sum;
-    }
-    __syncthreads();
-    if (tid < 16) {
-        float m = -INFINITY, sum = 0.f;
-        for (int k = 0; k < 16; ++k) {
-            const float v = s_m[tid][k];
-            if (v != -INFINITY) {
-                const float mn = fmaxf(m, v);
-                sum = sum * fast_exp2((m - mn) * kLog2e) + s_s[tid][k] * fast_exp2((v - mn) * kLog2e);
-                m = mn;
-            }
-        }
-        // lse of the row; -inf marks a row with no visible key
-        s_m[tid][16] = m == -INFINITY ? -INFINITY : m + fast_log2(sum) * kLn2;
-    }
-    __syncthreads();
-    // ---- phase 2: O = sum_j exp(lse_j - lse) O_j over NG groups of threads ----------
+    // ---- one pass: each of NG thread groups folds its share of the partials
+    // with a running maximum (lse and O of a partial are loaded together), then
+    // the groups are combined through LDS ----------------------------------------------
     int rp = 1;
     while (rp < rows) rp <<= 1;
-    const int NG = 256 / (16 * rp);
-    const int grp = tid / (16 * rp), rem = tid % (16 * rp);
-    const int rr = rem >> 4, d0 = (rem & 15) * 8;
-    const float L = rr < rows ? s_m[rr][16] : -INFINITY;
+    const int GS = CH * rp;  // threads per group: one per (row, 8-dim chunk)
+    const int NG = 256 / GS;
+    const int grp = tid / GS, rem = tid % GS;
+    const int rr = rem / CH, d0 = dsl * (D / DSPLIT) + (rem % CH) * 8;
+    float m = -INFINITY, sum = 0.f;
     f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    if (rr < rows && L != -INFINITY) {
+    if (rr < rows) {
 #pragma unroll 4
         for (int j = grp; j < n; j += NG) {
             const long long pr = prow0(j) + rr;
             const float v = a.part_lse[pr];
             const f32x4 o0 = *reinterpret_cast<const f32x4*>(a.part_o + pr * D + d0);
             const f32x4 o1 = *reinterpret_cast<const f32x4*>(a.part_o + pr * D + d0 + 4);
-            const float wgt = fast_exp2((v - L) * kLog2e);  // exp2(-inf) = 0 for an empty partial
-            acc0 += o0 * wgt;
-            acc1 += o1 * wgt;
+            if (v != -INFINITY) {  // -inf: a partial that saw no key
+                const float mn = fmaxf(m, v);
+                const float c = fast_exp2((m - mn) * kLog2e), wgt = fast_exp2((v - mn) * kLog2e);
+                acc0 = acc0 * c + o0 * wgt;
+                acc1 = acc1 * c + o1 * wgt;
+                sum = sum * c + wgt;
+                m = mn;
+            }
         }
     }
     if (NG > 1) {
         *reinterpret_cast<f32x4*>(&s_acc[tid][0]) = acc0;
         *reinterpret_cast<f32x4*>(&s_acc[tid][4]) = acc1;
+        s_gm[tid] = m;
+        s_gs[tid] = sum;
         __syncthreads();
         if (grp != 0) return;
-        for (int gq = 1; gq < NG; ++gq) {
-            acc0 += *reinterpret_cast<const f32x4*>(&s_acc[tid + gq * 16 * rp][0]);
-            acc1 += *reinterpret_cast<const f32x4*>(&s_acc[tid + gq * 16 * rp][4]);
+        float M = m;
+        for (int gq = 1; gq < NG; ++gq) M = fmaxf(M, s_gm[tid + gq * GS]);
+        if (M != -INFINITY) {
+            const float c = fast_exp2((m - M) * kLog2e);
+            acc0 *= c;
+            acc1 *= c;
+            sum *= c;
+            for (int gq = 1; gq < NG; ++gq) {
+                const int o = tid + gq * GS;
+                const float cg = fast_exp2((s_gm[o] - M) * kLog2e);  // 0 for an empty group
+                acc0 += *reinterpret_cast<const f32x4*>(&s_acc[o][0]) * cg;
+                acc1 += *reinterpret_cast<const f32x4*>(&s_acc[o][4]) * cg;
+                sum += s_gs[o] * cg;
+            }
         }
+        m = M;
     }
+    // lse of the row; -inf marks a row with no visible key (out = 0, lse = +inf)
+    const float inv = m == -INFINITY ? 0.f : 1.f / sum;
+    acc0 *= inv;
+    acc1 *= inv;
+    const float L = m == -INFINITY ? -INFINITY : m + fast_log2(sum) * kLn2;
     if (rr >= rows) return;
     const int i = rr / a.g, h = hk * a.g + rr % a.g;
     uint16_t* op = static_cast<uint16_t*>(a.out);
@@ -590,7 +590,7 @@ hipError_t launch_decode(const FwdArgs& a, int dtype, int grid, hipStream_t stre
 }
 
 hipError_t launch_decode_merge(const FwdArgs& a, int dtype, int grid, hipStream_t stream) {
-    const int segs = a.B * a.Hk;
+    const int segs = a.B * a.Hk * 4;  // DSPLIT workgroups per (sequence, kv head) segment
     if (dtype == DT_BF16)
         hipLaunchKernelGGL(fa_decode_merge_kernel<DT_BF16>, dim3(segs), dim3(256), 0, stream, a, grid * dec::NWAVE);
     else
