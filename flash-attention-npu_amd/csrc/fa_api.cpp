@@ -114,6 +114,7 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
     if (p->dropout_p != 0.f) return fail(FA_EUNSUPPORTED, "dropout is not supported (forward inference only)");
     FA_CHECK(p->softcap >= 0.f, "softcap must be >= 0");
     FA_CHECK(p->num_splits >= 0, "num_splits must be >= 0");
+    FA_CHECK(p->attention_chunk >= 0, "attention_chunk must be >= 0");
     FA_CHECK(p->seqlen_q >= 0, "seqlen_q must be >= 0");
     FA_CHECK(p->q && p->k && p->v && p->out && p->softmax_lse, "q, k, v, out and softmax_lse must be given");
     FA_CHECK(aligned16(p->q) && aligned16(p->k) && aligned16(p->v) && aligned16(p->out),
@@ -141,8 +142,15 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
                          p->batch_cache, p->batch);
         }
         FA_CHECK((p->k_new == nullptr) == (p->v_new == nullptr), "If key is supplied, value must also be passed in");
+        if (p->cache_leftpad)
+            FA_CHECK(!paged, "cache_leftpad is not supported with a paged KV cache (page_table / block_table)");
+        if (p->cu_seqlens_q) FA_CHECK(p->total_q >= 0, "total_q must be >= 0 with cu_seqlens_q");
+        if (p->cu_seqlens_k_new) {
+            FA_CHECK(p->k_new != nullptr, "cu_seqlens_k_new is given without new keys k / v");
+            FA_CHECK(p->total_k_new >= 0, "total_k_new must be >= 0 with cu_seqlens_k_new");
+        }
         if (p->k_new) {
-            FA_CHECK(p->seqlen_new >= 1, "k/v must have at least one new token");
+            FA_CHECK(p->cu_seqlens_k_new || p->seqlen_new >= 1, "k/v must have at least one new token");
             FA_CHECK(p->cache_seqlens != nullptr, "cache_seqlens is required to append k/v");
             FA_CHECK(aligned16(p->k_new) && aligned16(p->v_new), "k and v must be 16-byte aligned");
             FA_CHECK(strides8(p->knew_batch_stride, p->knew_row_stride, p->knew_head_stride) &&
@@ -161,6 +169,8 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
         }
     } else {
         FA_CHECK(p->k_new == nullptr && p->v_new == nullptr, "k_new/v_new are only valid for the kvcache forward");
+        FA_CHECK(!p->cache_leftpad && !p->cu_seqlens_k_new && !p->rotary_seqlens,
+                 "cache_leftpad, cu_seqlens_k_new and rotary_seqlens are only valid for the kvcache forward");
         FA_CHECK(p->rotary_cos == nullptr && p->rotary_sin == nullptr, "rotary is only valid for the kvcache forward");
         FA_CHECK(p->block_table == nullptr || kind == FA_KIND_VARLEN, "block_table is not valid for the dense forward");
         FA_CHECK(p->seqlen_k >= 0, "seqlen_k must be >= 0");
@@ -235,7 +245,8 @@ void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
     if (pl.allow_split) off = align256(off + sizeof(float) * (size_t)pl.items_max * pl.BM * pl.kd);
     pl.off_qrot = off;
     // decode reads a rotated copy of q; prefill rotates q as it loads it
-    if (pl.rotary && pl.decode) off = align256(off + 2 * (size_t)p->batch * p->seqlen_q * p->nheads * p->headdim);
+    const int64_t q_rows = (kind == FA_KIND_KVCACHE && p->cu_seqlens_q) ? p->total_q : (int64_t)p->batch * p->seqlen_q;
+    if (pl.rotary && pl.decode) off = align256(off + 2 * (size_t)q_rows * p->nheads * p->headdim);
     pl.total = off;
 }
 
@@ -266,7 +277,7 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
     // Decode without rotary appends inside the attention kernel; otherwise the
     // append (with the key rotation, and for decode the q rotation) runs as
     // its own launch first. Prefill rotates q inside its q load.
-    const bool fused_append = kind == FA_KIND_KVCACHE && p->k_new && pl.decode && !pl.rotary;
+    const bool fused_append = kind == FA_KIND_KVCACHE && p->k_new && pl.decode && !pl.rotary && !p->cu_seqlens_k_new;
     if (kind == FA_KIND_KVCACHE && p->k_new && !fused_append) {
         fa::KvPrepArgs k{};
         k.k_new = p->k_new;
@@ -314,6 +325,11 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
         k.Hk = p->nheads_k;
         k.D = p->headdim;
         k.Dv = p->headdim_v;
+        k.cu_knew = p->cu_seqlens_k_new;
+        k.total_new = p->cu_seqlens_k_new ? p->total_k_new : 0;
+        k.cu_q = p->cu_seqlens_q;
+        k.total_q = p->cu_seqlens_q ? p->total_q : 0;
+        k.rot_pos = pl.rotary ? p->rotary_seqlens : nullptr;
         hipError_t e = fa::launch_kv_prep(k, p->dtype, stream);
         if (e != hipSuccess) return fail(FA_EHIP, "kv_prep launch failed: %s", hipGetErrorString(e));
         if (pl.rotary && pl.decode) {
@@ -342,7 +358,8 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
     a.o_si = p->out_row_stride;
     a.o_sh = p->out_head_stride;
     a.lse = p->softmax_lse;
-    if (kind == FA_KIND_VARLEN) {
+    const bool ragged_q = kind == FA_KIND_VARLEN || (kind == FA_KIND_KVCACHE && p->cu_seqlens_q);
+    if (ragged_q) {
         a.lse_sb = 0;
         a.lse_sh = p->total_q;
     } else {
@@ -350,7 +367,7 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
         a.lse_sh = p->seqlen_q;
     }
     a.seqlens_k = kind == FA_KIND_DENSE ? nullptr : p->cache_seqlens;  // kvcache lengths / varlen seqused_k
-    a.cu_seqlens_q = kind == FA_KIND_VARLEN ? p->cu_seqlens_q : nullptr;
+    a.cu_seqlens_q = ragged_q ? p->cu_seqlens_q : nullptr;
     a.cu_seqlens_k = kind == FA_KIND_VARLEN ? p->cu_seqlens_k : nullptr;
     a.block_table = p->block_table;
     a.batch_idx = kind == FA_KIND_KVCACHE ? p->cache_batch_idx : nullptr;
@@ -367,7 +384,13 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
     a.Hk = p->nheads_k;
     a.g = pl.g;
     a.hd = p->headdim;
-    a.seqlen_new = (kind == FA_KIND_KVCACHE && p->k_new) ? p->seqlen_new : 0;
+    a.seqlen_new = (kind == FA_KIND_KVCACHE && p->k_new && !p->cu_seqlens_k_new) ? p->seqlen_new : 0;
+    if (kind == FA_KIND_KVCACHE) {
+        a.leftpad = p->cache_leftpad;
+        a.cu_knew = p->k_new ? p->cu_seqlens_k_new : nullptr;
+        a.rot_pos = pl.rotary ? p->rotary_seqlens : nullptr;
+    }
+    a.chunk = p->attention_chunk;
     if (fused_append) {
         a.k_new = p->k_new;
         a.kn_sb = p->knew_batch_stride;
@@ -447,6 +470,7 @@ fa_status_t validate_bwd(const fa_bwd_params* p, int kind) {
     FA_CHECK(p->headdim <= 256, "FlashAttention only supports head dimension at most 256");
     if (p->dropout_p != 0.f) return fail(FA_EUNSUPPORTED, "dropout is not supported");
     FA_CHECK(p->softcap >= 0.f, "softcap must be non-negative (0.0 disables softcap)");
+    FA_CHECK(p->attention_chunk >= 0, "attention_chunk must be >= 0");
     FA_CHECK(p->seqlen_q >= 0 && p->seqlen_k >= 0, "sequence lengths must be >= 0");
     FA_CHECK(p->q && p->k && p->v && p->out && p->dout && p->dq && p->dk && p->dv,
              "q, k, v, out, dout, dq, dk and dv must be given");
@@ -542,6 +566,7 @@ fa_status_t run_backward(const fa_bwd_params* p, int kind, void* stream_v) {
     if (p->is_causal) wr = 0;
     a.wl = wl;
     a.wr = wr;
+    a.chunk = p->attention_chunk;
     const int kd = p->headdim <= 128 ? 128 : 256;  // kernel head dim; dims above headdim read as zero
     const int64_t gkv = (int64_t)p->batch * p->nheads_k * ((p->seqlen_k + fa::bwd_key_block(kd) - 1) / fa::bwd_key_block(kd));
     const int64_t gq = (int64_t)p->batch * p->nheads_k *

@@ -183,7 +183,7 @@ __global__ void __launch_bounds__(256) fa_bwd_dsum_kernel(BwdArgs a, int dt) {
 }
 
 // ---- dK, dV ---------------------------------------------------------------------------------
-template <int DT, int HD, bool BIAS>
+template <int DT, int HD, bool BIAS, bool CHUNK>
 __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs a) {
     using C = BwCfg<HD>;
     constexpr int D = C::D, DCH = C::DCH, KSTEPS = C::KSTEPS, DBLK = C::DBLK, BK = C::BK, BQ = C::BQ,
@@ -256,6 +256,10 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
         int i_lo = 0, i_hi = bb.sq - 1;
         if (a.wr >= 0) i_lo = max(0, j0 - diag0 - a.wr);
         if (a.wl >= 0) i_hi = min(bb.sq - 1, j0 + BK - 1 - diag0 + a.wl);
+        if constexpr (CHUNK) {
+            i_lo = max(i_lo, row_lo(j0, a.wr, a.chunk) - diag0);
+            i_hi = min(i_hi, row_hi(j0 + BK - 1, a.wl, a.chunk) - diag0);
+        }
         const int r_lo = i_lo * g;
         const int r_hi = (i_hi >= i_lo) ? (i_hi + 1) * g : r_lo;
         const int ntiles = (r_hi - r_lo + BQ - 1) / BQ;
@@ -265,6 +269,21 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
         if (a.wr >= 0) wi_lo = max(0, jw - diag0 - a.wr);
         if (a.wl >= 0) wi_hi = min(bb.sq - 1, jw + WK - 1 - diag0 + a.wl);
         const bool wave_live = jw < bb.sk;
+        // CHUNK (attention_chunk): rows that see all of the wave's keys,
+        // [fc_lo, fc_hi], and the diagonal positions that see this lane's key
+        // of block rk, [kc_lo, kc_hi] (window and chunk together)
+        [[maybe_unused]] int fc_lo = 0, fc_hi = 0, kc_lo[KRB], kc_hi[KRB];
+        if constexpr (CHUNK) {
+            wi_lo = max(wi_lo, row_lo(jw, a.wr, a.chunk) - diag0);
+            wi_hi = min(wi_hi, row_hi(jw + WK - 1, a.wl, a.chunk) - diag0);
+            fc_lo = row_lo(jw + WK - 1, a.wr, a.chunk) - diag0;
+            fc_hi = row_hi(jw, a.wl, a.chunk) - diag0;
+#pragma unroll
+            for (int rk = 0; rk < KRB; ++rk) {
+                kc_lo[rk] = row_lo(jw + 16 * rk + li, a.wr, a.chunk);
+                kc_hi[rk] = row_hi(jw + 16 * rk + li, a.wl, a.chunk);
+            }
+        }
 
         f32x4 dka[KRB][DBLK], dva[KRB][DBLK];
 #pragma unroll
@@ -387,8 +406,12 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
                         if constexpr (MASK) {
                             const int dg = p4[t][e] + diag0;
                             bool vis = p4[t][e] >= 0 && jl < bb.sk;
-                            if (a.wl >= 0 && jl < dg - a.wl) vis = false;
-                            if (a.wr >= 0 && jl > dg + a.wr) vis = false;
+                            if constexpr (CHUNK) {
+                                vis = vis && dg >= kc_lo[rk] && dg <= kc_hi[rk];
+                            } else {
+                                if (a.wl >= 0 && jl < dg - a.wl) vis = false;
+                                if (a.wr >= 0 && jl > dg + a.wr) vis = false;
+                            }
                             pv = vis ? pv : 0.f;
                         }
                         float dsv = pv * (pacc[rk][t][e] - d4[t][e]) * a.scale;
@@ -436,6 +459,9 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
                     bool full = h0 + 32 <= r_hi && jw + WK <= bb.sk;
                     if (a.wr >= 0 && jw + WK - 1 > p_lo + diag0 + a.wr) full = false;
                     if (a.wl >= 0 && jw < p_hi + diag0 - a.wl) full = false;
+                    if constexpr (CHUNK) {
+                        if (p_lo < fc_lo || p_hi > fc_hi) full = false;
+                    }
                     if (full) half(buf, hh, std::integral_constant<bool, false>{});
                     else half(buf, hh, std::integral_constant<bool, true>{});
                 }
@@ -520,8 +546,8 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
         int k_lo = 0, k_hi = bb.sk;
         {
             const int i_lo = tile_row0 / g, i_hi = (tile_row0 + tile_rows - 1) / g;
-            if (a.wl >= 0) k_lo = max(0, i_lo + diag0 - a.wl);
-            if (a.wr >= 0) k_hi = min(bb.sk, i_hi + diag0 + a.wr + 1);
+            k_lo = max(0, key_lo(i_lo + diag0, a.wl, a.chunk));
+            k_hi = min(bb.sk, key_hi(i_hi + diag0, a.wr, a.chunk) + 1);
             if (k_hi < k_lo) k_hi = k_lo;
         }
         const int ntiles = (k_hi - k_lo + BN - 1) / BN;
@@ -530,6 +556,9 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
         const bool wave_live = wrows > 0;
         const int wi_lo = wave_live ? wrow0 / g : 0;
         const int wi_hi = wave_live ? (wrow0 + wrows - 1) / g : 0;
+        // keys visible to some row of the wave: [w_lo, w_hi]; to every row: [f_lo, f_hi]
+        const int w_lo = key_lo(wi_lo + diag0, a.wl, a.chunk), w_hi = key_hi(wi_hi + diag0, a.wr, a.chunk);
+        const int f_lo = key_lo(wi_hi + diag0, a.wl, a.chunk), f_hi = key_hi(wi_lo + diag0, a.wr, a.chunk);
 
         const int64_t qbase = a.cu_seqlens_q ? (int64_t)a.cu_seqlens_q[b] * a.q_si : (int64_t)b * a.q_sb;
         const int64_t dobase = a.cu_seqlens_q ? (int64_t)a.cu_seqlens_q[b] * a.do_si : (int64_t)b * a.do_sb;
@@ -539,7 +568,7 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
         // q and dout rows as B operands; lse (log2 units) and dsum per row
         u32x4 qreg[RB][KSTEPS], dreg[RB][KSTEPS];
         float lse2[RB], dsv[RB], slope[RB];
-        int qi[RB];
+        int qi[RB], rlo[RB], rhi[RB];  // rlo/rhi: the row's visible keys before the clamp to k_hi
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             const int r = wrow0 + rb * 16 + li;
@@ -547,6 +576,8 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
             const int i = ok ? r / g : 0;
             const int h = hk * g + (ok ? r % g : 0);
             qi[rb] = i;
+            rlo[rb] = key_lo(i + diag0, a.wl, a.chunk);
+            rhi[rb] = key_hi(i + diag0, a.wr, a.chunk);
             const int64_t lo = a.cu_seqlens_q ? (int64_t)h * a.lse_sh + a.cu_seqlens_q[b] + i
                                               : (int64_t)b * a.lse_sb + (int64_t)h * a.lse_sh + i;
             lse2[rb] = ok ? a.lse[lo] * kLog2e : INFINITY;
@@ -634,10 +665,7 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
                         const float x = bw_score<BIAS>(a, sacc[rb][kb][e], slope[rb], qi[rb] + diag0 - j, th);
                         float pv = fast_exp2(x - lse2[rb]);
                         if constexpr (MASK) {
-                            const int dg = qi[rb] + diag0;
-                            bool vis = j < k_hi;
-                            if (a.wl >= 0 && j < dg - a.wl) vis = false;
-                            if (a.wr >= 0 && j > dg + a.wr) vis = false;
+                            const bool vis = j < k_hi && j >= rlo[rb] && j <= rhi[rb];
                             pv = vis ? pv : 0.f;
                         }
                         float d = pv * (pacc[rb][kb][e] - dsv[rb]) * a.scale;
@@ -668,20 +696,13 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
         for (int t = 0; t < ntiles; ++t) {
             const int buf = t & 1;
             const int s0 = k_lo + t * BN, s1 = s0 + BN;
-            bool skip = !wave_live;
-            if (a.wr >= 0 && s0 > wi_hi + diag0 + a.wr) skip = true;
-            if (a.wl >= 0 && s1 - 1 < wi_lo + diag0 - a.wl) skip = true;
+            const bool skip = !wave_live || s0 > w_hi || s1 - 1 < w_lo;
             if (!skip) {
 #pragma unroll
                 for (int hh = 0; hh < BN / 32; ++hh) {
                     const int h0 = s0 + 32 * hh, h1 = h0 + 32;
-                    bool hskip = h0 >= k_hi;
-                    if (a.wr >= 0 && h0 > wi_hi + diag0 + a.wr) hskip = true;
-                    if (a.wl >= 0 && h1 - 1 < wi_lo + diag0 - a.wl) hskip = true;
-                    if (hskip) continue;
-                    bool full = h1 <= k_hi;
-                    if (a.wl >= 0 && h0 < wi_hi + diag0 - a.wl) full = false;
-                    if (a.wr >= 0 && h1 - 1 > wi_lo + diag0 + a.wr) full = false;
+                    if (h0 >= k_hi || h0 > w_hi || h1 - 1 < w_lo) continue;
+                    const bool full = h1 <= k_hi && h0 >= f_lo && h1 - 1 <= f_hi;
                     if (full) half(buf, hh, h0, std::integral_constant<bool, false>{});
                     else half(buf, hh, h0, std::integral_constant<bool, true>{});
                 }
@@ -712,9 +733,15 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
 }
 
 // ---- host-side launchers (called from fa_api.cpp) -------------------------------------------
+// attention_chunk runs the dK/dV kernel's CHUNK instance (on the general score
+// path); the common instances keep the plain window masks, whose code the
+// chunk tests would slow down.
 template <int DT, int HD, bool BIAS>
 static void launch_bwd_t(const BwdArgs& a, int grid_kv, int grid_q, hipStream_t stream) {
-    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<DT, HD, BIAS>), dim3(grid_kv), dim3(BwCfg<HD>::KNT), 0, stream, a);
+    if (a.chunk > 0)
+        hipLaunchKernelGGL((fa_bwd_dkdv_kernel<DT, HD, true, true>), dim3(grid_kv), dim3(BwCfg<HD>::KNT), 0, stream, a);
+    else
+        hipLaunchKernelGGL((fa_bwd_dkdv_kernel<DT, HD, BIAS, false>), dim3(grid_kv), dim3(BwCfg<HD>::KNT), 0, stream, a);
     hipLaunchKernelGGL((fa_bwd_dq_kernel<DT, HD, BIAS>), dim3(grid_q), dim3(BwCfg<HD>::QNT), 0, stream, a);
 }
 

@@ -84,4 +84,53 @@ __device__ __forceinline__ float wave_sum16x4(float v) {
     return v;
 }
 
+// Sequence of ragged row T: the largest b < B with cu[b] <= T (cu is a
+// non-decreasing prefix of B + 1 entries).
+__device__ __forceinline__ int seq_of(const int* cu, int B, int T) {
+    int lo = 0, hi = B;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (cu[mid] <= T) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// First key of the attention chunk that holds diagonal position p (chunk > 0):
+// chunk * floor(p / chunk), also for negative p.
+__device__ __forceinline__ int chunk_start(int p, int chunk) {
+    const int q = p >= 0 ? p / chunk : -((-p + chunk - 1) / chunk);
+    return q * chunk;
+}
+
+// Keys visible to the query whose diagonal position is d (d = i + Sk - Sq,
+// bottom-right aligned) are [key_lo(d), key_hi(d)] intersected with [0, Sk):
+// the local window (wl / wr, -1 = unbounded, causal is wr = 0) and, with
+// attention_chunk c > 0, the chunk [chunk_start(d), chunk_start(d) + c).
+// Both bounds are non-decreasing in d, so a run of rows sees at most
+// [key_lo(first row), key_hi(last row)].
+__device__ __forceinline__ int key_lo(int d, int wl, int chunk) {
+    int lo = wl >= 0 ? d - wl : -0x3fffffff;
+    if (chunk > 0) lo = max(lo, chunk_start(d, chunk));
+    return lo;
+}
+__device__ __forceinline__ int key_hi(int d, int wr, int chunk) {
+    int hi = wr >= 0 ? d + wr : 0x3fffffff;
+    if (chunk > 0) hi = min(hi, chunk_start(d, chunk) + chunk - 1);
+    return hi;
+}
+
+// The inverse view: key j is visible to the queries whose diagonal position d
+// lies in [row_lo(j), row_hi(j)] (non-decreasing in j as well).
+__device__ __forceinline__ int row_lo(int j, int wr, int chunk) {
+    int lo = wr >= 0 ? j - wr : -0x3fffffff;
+    if (chunk > 0) lo = max(lo, chunk_start(j, chunk));
+    return lo;
+}
+__device__ __forceinline__ int row_hi(int j, int wl, int chunk) {
+    int hi = wl >= 0 ? j + wl : 0x3fffffff;
+    if (chunk > 0) hi = min(hi, chunk_start(j, chunk) + chunk - 1);
+    return hi;
+}
+
 }  // namespace fa

@@ -39,23 +39,26 @@ struct DecSeg {
     int b, hk;
     int lo_tile;      // first 32-key tile of the sequence's visible key range
     int sk, sq, crow;
+    int lp;           // cache_leftpad: key j is cache row lp + j (contiguous caches)
 };
 
 // Per-batch facts kept in LDS: first tile, key count, query count, cache row.
 struct DecBatch {
-    int lo_tile, sk, sq, crow;
+    int lo_tile, sk, sq, crow, lp;
 };
 
 __device__ __forceinline__ void dec_batch(const FwdArgs& a, int b, DecBatch& d, int& ntiles) {
     int sq = a.cu_seqlens_q ? a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b] : a.Sq;
     int sk;
-    if (a.seqlens_k) sk = a.seqlens_k[b] + a.seqlen_new;
+    const int lp = a.leftpad ? min(max(a.leftpad[b], 0), a.kv_capacity) : 0;
+    if (a.seqlens_k) sk = a.seqlens_k[b] + (a.cu_knew ? a.cu_knew[b + 1] - a.cu_knew[b] : a.seqlen_new) - lp;
     else if (a.cu_seqlens_k) sk = a.cu_seqlens_k[b + 1] - a.cu_seqlens_k[b];
     else sk = a.Sk;
     sq = min(max(sq, 0), a.Sq);
-    sk = min(max(sk, 0), a.kv_capacity);
-    int lo = a.wl >= 0 ? max(0, sk - sq - a.wl) : 0;
-    int hi = a.wr >= 0 ? min(sk, sk - 1 + a.wr + 1) : sk;
+    sk = min(max(sk, 0), a.kv_capacity - lp);
+    const int lo = max(0, key_lo(sk - sq, a.wl, a.chunk));
+    const int hi = min(sk, key_hi(sk - 1, a.wr, a.chunk) + 1);
+    d.lp = lp;
     d.sq = sq;
     d.sk = sk;
     d.lo_tile = lo / dec::KT;
@@ -82,6 +85,7 @@ __device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref
     s.sk = d.sk;
     s.sq = d.sq;
     s.crow = d.crow;
+    s.lp = d.lp;
     return s;
 }
 
@@ -179,7 +183,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             return base + (int64_t)b2 * sb + (int64_t)inpage * si + (int64_t)s.hk * sh;
         }
         if (LAYOUT == 2 && a.cu_seqlens_k) return base + ((int64_t)a.cu_seqlens_k[s.b] + key) * si + (int64_t)s.hk * sh;
-        return base + (int64_t)s.crow * sb + (int64_t)key * si + (int64_t)s.hk * sh;
+        return base + (int64_t)s.crow * sb + (int64_t)(s.lp + key) * si + (int64_t)s.hk * sh;
     };
 
     // With a fused append, keys >= sk - seqlen_new come from k_new / v_new; the
@@ -240,9 +244,12 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     f32x4 oacc[DBLK];
     float m_run, l_run;
     int rows = 0;
+    int seg_flo = 0, seg_fhi = 0;  // keys visible to every row of the segment: [seg_flo, seg_fhi]
 
     auto begin_seg = [&](const DecSeg& s) {
         rows = s.sq * a.g;
+        seg_flo = key_lo(s.sk - 1, a.wl, a.chunk);       // last row (diagonal sk - 1)
+        seg_fhi = key_hi(s.sk - s.sq, a.wr, a.chunk);    // first row
         const bool ok = li < rows;
         const int i = ok ? li / a.g : 0;
         const int h = s.hk * a.g + (ok ? li % a.g : 0);
@@ -337,10 +344,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         }
         // online softmax (log2 domain), row = li, keys key0 + 16h + 4G + e
         const int sk = cs.sk, diag0 = cs.sk - cs.sq;
-        const int imax = (rows - 1) / a.g;
-        bool full = key0 + KT <= sk;
-        if (a.wl >= 0 && key0 < imax + diag0 - a.wl) full = false;
-        if (a.wr >= 0 && key0 + KT - 1 > diag0 + a.wr) full = false;
+        const bool full = key0 + KT <= sk && key0 >= seg_flo && key0 + KT - 1 <= seg_fhi;
         constexpr bool plain = !BIAS;
         float x[2][4];
 #pragma unroll
@@ -365,14 +369,13 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             }
         if (!full) {
             const int dg = qi + diag0;
+            const int rlo = key_lo(dg, a.wl, a.chunk), rhi = key_hi(dg, a.wr, a.chunk);
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int j = key0 + h * 16 + G * 4 + e;
-                    bool vis = j < sk;
-                    if (a.wl >= 0 && j < dg - a.wl) vis = false;
-                    if (a.wr >= 0 && j > dg + a.wr) vis = false;
+                    const bool vis = j < sk && j >= rlo && j <= rhi;
                     x[h][e] = vis ? x[h][e] : -INFINITY;
                 }
         }

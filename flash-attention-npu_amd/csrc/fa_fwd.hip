@@ -47,6 +47,7 @@ constexpr int kMaxBatchLds = 2048;
 struct BatchInfo {
     int sq, sk, rows, mt, lo, hi;
     int len0;  // kvcache: cache_seqlens[b] before this call's append, else 0
+    int lp;    // kvcache: cache_leftpad[b] (key j is cache row lp + j), else 0
 };
 
 template <int BM>
@@ -54,18 +55,20 @@ __device__ __forceinline__ void batch_info(const FwdArgs& a, int b, BatchInfo& b
     int sq = a.cu_seqlens_q ? a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b] : a.Sq;
     int sk;
     bi.len0 = a.seqlens_k ? a.seqlens_k[b] : 0;
-    if (a.seqlens_k) sk = bi.len0 + a.seqlen_new;  // cache_seqlens / seqused_k
+    bi.lp = a.leftpad ? min(max(a.leftpad[b], 0), a.kv_capacity) : 0;
+    if (a.seqlens_k)  // cache_seqlens (+ this call's new tokens) / seqused_k
+        sk = bi.len0 + (a.cu_knew ? a.cu_knew[b + 1] - a.cu_knew[b] : a.seqlen_new) - bi.lp;
     else if (a.cu_seqlens_k) sk = a.cu_seqlens_k[b + 1] - a.cu_seqlens_k[b];
     else sk = a.Sk;
     sq = min(max(sq, 0), a.Sq);  // Sq is max_seqlen_q for varlen: bounds the tiles
-    sk = min(max(sk, 0), a.kv_capacity);
+    sk = min(max(sk, 0), a.kv_capacity - bi.lp);
     bi.sq = sq;
     bi.sk = sk;
     bi.rows = sq * a.g;
     bi.mt = (bi.rows + BM - 1) / BM;
     // union of the keys visible to any row of this sequence
-    int lo = a.wl >= 0 ? max(0, sk - sq - a.wl) : 0;
-    int hi = a.wr >= 0 ? min(sk, sk - 1 + a.wr + 1) : sk;
+    const int lo = max(0, key_lo(sk - sq, a.wl, a.chunk));
+    const int hi = min(sk, key_hi(sk - 1, a.wr, a.chunk) + 1);
     bi.lo = lo;
     bi.hi = max(hi, lo);
 }
@@ -269,8 +272,8 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
         int k_lo, k_hi;
         {
             const int i_lo = tile_row0 / g, i_hi = (tile_row0 + tile_rows - 1) / g;
-            k_lo = a.wl >= 0 ? max(0, i_lo + diag0 - a.wl) : 0;
-            k_hi = a.wr >= 0 ? min(bi.sk, i_hi + diag0 + a.wr + 1) : bi.sk;
+            k_lo = max(0, key_lo(i_lo + diag0, a.wl, a.chunk));
+            k_hi = min(bi.sk, key_hi(i_hi + diag0, a.wr, a.chunk) + 1);
             if (ns > 1) {
                 const int c0 = bi.lo + split * chunk;
                 k_lo = max(k_lo, c0);
@@ -285,6 +288,9 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
         const bool wave_live = wrows > 0;
         const int wi_lo = wave_live ? wrow0 / g : 0;
         const int wi_hi = wave_live ? (wrow0 + wrows - 1) / g : 0;
+        // keys visible to some row of the wave: [w_lo, w_hi]; to every row: [f_lo, f_hi]
+        const int w_lo = key_lo(wi_lo + diag0, a.wl, a.chunk), w_hi = key_hi(wi_hi + diag0, a.wr, a.chunk);
+        const int f_lo = key_lo(wi_hi + diag0, a.wl, a.chunk), f_hi = key_hi(wi_lo + diag0, a.wr, a.chunk);
 
         // ---- K/V tiles: registers -> double-buffered LDS ----------------------------------
         u32x4 kr[CPT], vr[CPT];
@@ -296,8 +302,10 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
         if constexpr (PAGED) {
             btrow = a.block_table + (int64_t)crow * a.bt_stride;
         } else {
-            const int64_t row0k = a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.k_si : (int64_t)crow * a.k_sb;
-            const int64_t row0v = a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.v_si : (int64_t)crow * a.v_sb;
+            const int64_t row0k = a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.k_si
+                                                 : (int64_t)crow * a.k_sb + (int64_t)bi.lp * a.k_si;
+            const int64_t row0v = a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.v_si
+                                                 : (int64_t)crow * a.v_sb + (int64_t)bi.lp * a.v_si;
             kb0 += row0k;
             vb0 += row0v;
         }
@@ -358,6 +366,13 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
             qrows[rb] = qrow;
             qok[rb] = ok;
         }
+        // each row's visible keys [rlo, rhi] (before the clamp to k_hi)
+        int rlo[RB], rhi[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            rlo[rb] = key_lo(qi[rb] + diag0, a.wl, a.chunk);
+            rhi[rb] = key_hi(qi[rb] + diag0, a.wr, a.chunk);
+        }
         if constexpr (ROT) {
             // q[b, i] is rotated at cache_seqlens[b] (+ i when causal or local).
             // The rotary arguments are read from the argument block here (the
@@ -379,7 +394,7 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
                 RopeOps rop[RB][KSTEPS];
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb) {
-                    int pos = bi.len0 + (rk->rot_same_pos ? 0 : qi[rb]);
+                    int pos = (rk->rot_pos ? rk->rot_pos[b] : bi.len0) + (rk->rot_same_pos ? 0 : qi[rb]);
                     pos = min(max(pos, 0), rk->seqlen_ro - 1);
                     const uint16_t* crow_c = static_cast<const uint16_t*>(rk->rot_cos) + (int64_t)pos * (rot_rd >> 1);
                     const uint16_t* crow_s = static_cast<const uint16_t*>(rk->rot_sin) + (int64_t)pos * (rot_rd >> 1);
@@ -473,10 +488,7 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
                             x = y * kLog2e;
                         }
                         if constexpr (MASK) {
-                            const int dg = qi[rb] + diag0;
-                            bool vis = j < k_hi;
-                            if (a.wl >= 0 && j < dg - a.wl) vis = false;
-                            if (a.wr >= 0 && j > dg + a.wr) vis = false;
+                            const bool vis = j < k_hi && j >= rlo[rb] && j <= rhi[rb];
                             x = vis ? x : -INFINITY;
                         }
                         sacc[rb][kb][e] = x;
@@ -541,21 +553,13 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
         for (int t = 0; t < ntiles; ++t) {
             const int buf = t & 1;
             const int s0 = k_lo + t * BN, s1 = s0 + BN;
-            bool skip = !wave_live;
-            if (a.wr >= 0 && s0 > wi_hi + diag0 + a.wr) skip = true;
-            if (a.wl >= 0 && s1 - 1 < wi_lo + diag0 - a.wl) skip = true;
+            const bool skip = !wave_live || s0 > w_hi || s1 - 1 < w_lo;
             if (!skip) {
 #pragma unroll
                 for (int hh = 0; hh < BN / 32; ++hh) {
                     const int h0 = s0 + 32 * hh, h1 = h0 + 32;
-                    bool hskip = false;
-                    if (a.wr >= 0 && h0 > wi_hi + diag0 + a.wr) hskip = true;
-                    if (a.wl >= 0 && h1 - 1 < wi_lo + diag0 - a.wl) hskip = true;
-                    if (h0 >= k_hi) hskip = true;
-                    if (hskip) continue;
-                    bool full = h1 <= k_hi;
-                    if (a.wl >= 0 && h0 < wi_hi + diag0 - a.wl) full = false;
-                    if (a.wr >= 0 && h1 - 1 > wi_lo + diag0 + a.wr) full = false;
+                    if (h0 > w_hi || h1 - 1 < w_lo || h0 >= k_hi) continue;
+                    const bool full = h1 <= k_hi && h0 >= f_lo && h1 - 1 <= f_hi;
                     if (full) tile(buf, hh, h0, std::integral_constant<bool, false>{});
                     else tile(buf, hh, h0, std::integral_constant<bool, true>{});
                 }

@@ -67,6 +67,13 @@ struct FwdArgs {
     const void* rot_cos;
     const void* rot_sin;
     int rot_dim, rot_interleaved, rot_same_pos, seqlen_ro;
+    // kvcache: first valid cache row per sequence (keys are rows leftpad + j);
+    // per-sequence new-token counts cu_knew[b+1] - cu_knew[b] (else seqlen_new);
+    // rotary position base per sequence (else cache_seqlens)
+    const int* leftpad;
+    const int* cu_knew;
+    const int* rot_pos;
+    int chunk;          // attention_chunk, 0 = off
 };
 
 // Backward (dense / varlen). Row layouts as in FwdArgs; lse and dsum share
@@ -102,6 +109,7 @@ struct BwdArgs {
     int hd;             // head dim in memory (<= the kernel's)
     int total_q;        // varlen: rows of q
     int wl, wr;         // normalised window, -1 = unbounded, causal => wr = 0
+    int chunk;          // attention_chunk, 0 = off
 };
 
 struct KvPrepArgs {
@@ -130,6 +138,12 @@ struct KvPrepArgs {
     void* q_out;
     int q_same_pos;
     int B, S_new, Sq, H, Hk, D, Dv;
+    // ragged layouts: new tokens (total_new, Hk, D) split by cu_knew, q
+    // (total_q, H, D) split by cu_q; rotary position base per sequence
+    const int* cu_knew;
+    const int* cu_q;
+    const int* rot_pos;
+    int total_new, total_q;
 };
 
 }  // namespace fa

@@ -6,8 +6,11 @@
 // (flash_attn_npu_v2/interface_arch22.py:1452-1538 in the reference; the
 // reference kernels accept k/v and cache_batch_idx but ignore them and reject
 // rotary: csrc/arch22/flash_attn_npu_v2/flash_api.cpp:415-436):
-//   cache[idx(b), L_b + t] = rope(k[b, t], pos = L_b + t),  t < S_new
-//   q[b, i] rotated at L_b + i (causal or local) or at L_b (otherwise)
+//   cache[idx(b), L_b + t] = rope(k[b, t], pos = P_b + t),  t < S_new(b)
+//   q[b, i] rotated at P_b + i (causal or local) or at P_b (otherwise)
+// with P_b = rotary_seqlens[b] when given, else L_b (the v3 docstring,
+// README.md:311-401 of the reference). New tokens and q may be ragged
+// ((total, heads, D) split by cu_seqlens_k_new / cu_seqlens_q).
 // The rotation itself is rope_chunk (fa_rope.h). Prefill rotates q inside
 // its own q load, so only decode asks for q_out here.
 #include "fa_common.h"
@@ -38,20 +41,38 @@ __global__ void __launch_bounds__(256) fa_kv_prep_kernel(KvPrepArgs a) {
     uint16_t* dst;
     int pos;
     if (which == 2) {
-        if (row >= a.B * a.Sq * a.H) return;
         const int h = row % a.H;
         const int bi = row / a.H;
-        const int i = bi % a.Sq;
-        const int b = bi / a.Sq;
-        src = static_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_sb + (int64_t)i * a.q_si + (int64_t)h * a.q_sh;
+        int b, i;
+        if (a.cu_q) {  // ragged q: row bi of (total_q, H, D)
+            if (row >= a.total_q * a.H) return;
+            b = seq_of(a.cu_q, a.B, bi);
+            i = bi - a.cu_q[b];
+            src = static_cast<const uint16_t*>(a.q) + (int64_t)bi * a.q_si + (int64_t)h * a.q_sh;
+        } else {
+            if (row >= a.B * a.Sq * a.H) return;
+            i = bi % a.Sq;
+            b = bi / a.Sq;
+            src = static_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_sb + (int64_t)i * a.q_si + (int64_t)h * a.q_sh;
+        }
         dst = static_cast<uint16_t*>(a.q_out) + (int64_t)row * a.D;
-        pos = (a.seqlens ? a.seqlens[b] : 0) + (a.q_same_pos ? 0 : i);
+        pos = (a.rot_pos ? a.rot_pos[b] : a.seqlens ? a.seqlens[b] : 0) + (a.q_same_pos ? 0 : i);
     } else {
-        if (row >= a.B * a.S_new * a.Hk) return;
         const int h = row % a.Hk;
         const int bt = row / a.Hk;
-        const int t = bt % a.S_new;
-        const int b = bt / a.S_new;
+        int b, t;
+        int64_t src_off;
+        if (a.cu_knew) {  // ragged new tokens: row bt of (total_new, Hk, D)
+            if (row >= a.total_new * a.Hk) return;
+            b = seq_of(a.cu_knew, a.B, bt);
+            t = bt - a.cu_knew[b];
+            src_off = (int64_t)bt * (which == 0 ? a.kn_si : a.vn_si);
+        } else {
+            if (row >= a.B * a.S_new * a.Hk) return;
+            t = bt % a.S_new;
+            b = bt / a.S_new;
+            src_off = which == 0 ? (int64_t)b * a.kn_sb + (int64_t)t * a.kn_si : (int64_t)b * a.vn_sb + (int64_t)t * a.vn_si;
+        }
         const int j = a.seqlens[b] + t;
         if (j < 0 || j >= a.kv_capacity) return;  // cache too small: nothing is written
         const int crow = a.batch_idx ? a.batch_idx[b] : b;
@@ -67,11 +88,9 @@ __global__ void __launch_bounds__(256) fa_kv_prep_kernel(KvPrepArgs a) {
             if (crow < 0 || crow >= a.batch_cache) return;
             dst = cache + (int64_t)crow * sb + (int64_t)j * si + (int64_t)h * sh;
         }
-        src = which == 0 ? static_cast<const uint16_t*>(a.k_new) + (int64_t)b * a.kn_sb + (int64_t)t * a.kn_si +
-                               (int64_t)h * a.kn_sh
-                         : static_cast<const uint16_t*>(a.v_new) + (int64_t)b * a.vn_sb + (int64_t)t * a.vn_si +
-                               (int64_t)h * a.vn_sh;
-        pos = j;
+        src = which == 0 ? static_cast<const uint16_t*>(a.k_new) + src_off + (int64_t)h * a.kn_sh
+                         : static_cast<const uint16_t*>(a.v_new) + src_off + (int64_t)h * a.vn_sh;
+        pos = a.rot_pos ? a.rot_pos[b] + t : j;
     }
     u32x4 x = *reinterpret_cast<const u32x4*>(src + 8 * u);
     if (8 * u < rd) {
@@ -83,8 +102,8 @@ __global__ void __launch_bounds__(256) fa_kv_prep_kernel(KvPrepArgs a) {
 }
 
 hipError_t launch_kv_prep(const KvPrepArgs& a, int dtype, hipStream_t stream) {
-    const int64_t rows_kv = a.k_new ? (int64_t)a.B * a.S_new * a.Hk : 0;
-    const int64_t rows_q = a.q_out ? (int64_t)a.B * a.Sq * a.H : 0;
+    const int64_t rows_kv = !a.k_new ? 0 : a.cu_knew ? (int64_t)a.total_new * a.Hk : (int64_t)a.B * a.S_new * a.Hk;
+    const int64_t rows_q = !a.q_out ? 0 : a.cu_q ? (int64_t)a.total_q * a.H : (int64_t)a.B * a.Sq * a.H;
     if (rows_kv >= INT32_MAX || rows_q >= INT32_MAX) return hipErrorInvalidValue;
     const int rpb = 256 / ((a.D > a.Dv ? a.D : a.Dv) >> 3);
     const int64_t mx = rows_kv > rows_q ? rows_kv : rows_q;

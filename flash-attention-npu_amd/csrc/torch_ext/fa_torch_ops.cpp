@@ -1,6 +1,7 @@
 // fa_torch_ops.cpp -- PyTorch-ROCm operators over the C ABI (libfa_mi355x.so).
 //
-// Registers torch.ops.fa_mi355x.{fwd_kvcache, fwd, varlen_fwd, fwd_combine, bwd, varlen_bwd}.
+// Registers torch.ops.fa_mi355x.{fwd_kvcache, fwd_kvcache_v3, fwd, varlen_fwd, fwd_combine, bwd,
+// varlen_bwd}.
 // Argument order and meaning follow the reference pybind entry points
 // (csrc/arch22/flash_attn_npu_v2/flash_api.cpp: mha_fwd_kvcache :356-377,
 // mha_fwd :628-640, mha_varlen_fwd :828-850, bound at :1301-1309). Unlike the
@@ -72,12 +73,18 @@ void set_alibi(fa_fwd_params& p, const OptT& alibi, const Tensor& q, int64_t bat
 }
 
 // ---- flash_attn_with_kvcache -----------------------------------------------------------
-std::tuple<Tensor, Tensor> fwd_kvcache(const Tensor& q, Tensor& kcache, Tensor& vcache, const OptT& k_new,
-                                       const OptT& v_new, const OptT& seqlens_k, const OptT& rotary_cos,
-                                       const OptT& rotary_sin, const OptT& cache_batch_idx, const OptT& leftpad_k,
-                                       const OptT& block_table, const OptT& alibi_slopes, double softmax_scale,
-                                       bool is_causal, int64_t window_size_left, int64_t window_size_right,
-                                       double softcap, bool is_rotary_interleaved, int64_t num_splits) {
+// Shared by the v2 op (the reference's fwd_kvcache argument order) and the v3
+// op, which adds ragged queries / new tokens, rotary positions and
+// attention_chunk. q is (B, Sq, H, D), or (total_q, H, D) with cu_seqlens_q;
+// k / v are (B, S_new, Hk, D), or (total_k_new, Hk, D) with cu_seqlens_k_new.
+std::tuple<Tensor, Tensor> kvcache_impl(const Tensor& q, Tensor& kcache, Tensor& vcache, const OptT& k_new,
+                                        const OptT& v_new, const OptT& seqlens_k, const OptT& rotary_cos,
+                                        const OptT& rotary_sin, const OptT& cache_batch_idx, const OptT& leftpad_k,
+                                        const OptT& block_table, const OptT& alibi_slopes, const OptT& cu_seqlens_q,
+                                        const OptT& cu_seqlens_k_new, int64_t max_seqlen_q,
+                                        const OptT& rotary_seqlens, double softmax_scale, bool is_causal,
+                                        int64_t window_size_left, int64_t window_size_right, int64_t attention_chunk,
+                                        double softcap, bool is_rotary_interleaved, int64_t num_splits) {
     c10::DeviceGuard guard(q.device());
     TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
     check_dev(kcache, q, "k_cache");
@@ -85,19 +92,24 @@ std::tuple<Tensor, Tensor> fwd_kvcache(const Tensor& q, Tensor& kcache, Tensor& 
     const int32_t dt = dtype_code(q);
     TORCH_CHECK(kcache.scalar_type() == q.scalar_type() && vcache.scalar_type() == q.scalar_type(),
                 "query and key/value must have the same dtype");
-    TORCH_CHECK(q.dim() == 4, "q must have shape (batch_size, seqlen_q, num_heads, head_size)");
+    const bool ragged_q = cu_seqlens_q.has_value();
+    if (ragged_q) {
+        TORCH_CHECK(q.dim() == 3, "q must have shape (total_q, num_heads, head_size) with cu_seqlens_q");
+    } else {
+        TORCH_CHECK(q.dim() == 4, "q must have shape (batch_size, seqlen_q, num_heads, head_size)");
+    }
     TORCH_CHECK(kcache.dim() == 4 && vcache.dim() == 4, "k_cache/v_cache must be 4-dimensional");
     TORCH_CHECK(q.stride(-1) == 1 && kcache.stride(-1) == 1 && vcache.stride(-1) == 1,
                 "Input tensor must have contiguous last dimension");
-    TORCH_CHECK(!leftpad_k.has_value(), "cache_leftpad is not supported");
     const bool paged = block_table.has_value();
+    const int64_t batch = ragged_q ? cu_seqlens_q->numel() - 1 : q.size(0);
+    TORCH_CHECK(batch >= 1, "batch size must be positive");
     fa_fwd_params p{};
     p.abi_version = FA_MI355X_ABI_VERSION;
     p.dtype = dt;
-    p.batch = (int32_t)q.size(0);
-    p.seqlen_q = (int32_t)q.size(1);
-    p.nheads = (int32_t)q.size(2);
-    p.headdim = (int32_t)q.size(3);
+    p.batch = (int32_t)batch;
+    p.nheads = (int32_t)q.size(-2);
+    p.headdim = (int32_t)q.size(-1);
     p.nheads_k = (int32_t)kcache.size(2);
     p.headdim_v = (int32_t)vcache.size(3);
     TORCH_CHECK(kcache.size(3) == p.headdim, "k_cache head size must match q");
@@ -105,9 +117,19 @@ std::tuple<Tensor, Tensor> fwd_kvcache(const Tensor& q, Tensor& kcache, Tensor& 
     p.batch_cache = (int32_t)kcache.size(0);
     p.seqlen_k = (int32_t)kcache.size(1);
     p.q = q.data_ptr();
-    p.q_batch_stride = q.stride(0);
-    p.q_row_stride = q.stride(1);
-    p.q_head_stride = q.stride(2);
+    if (ragged_q) {
+        p.cu_seqlens_q = i32_ptr(cu_seqlens_q, q, "cu_seqlens_q");
+        p.seqlen_q = (int32_t)max_seqlen_q;
+        p.total_q = (int32_t)q.size(0);
+        p.q_batch_stride = 0;
+        p.q_row_stride = q.stride(0);
+        p.q_head_stride = q.stride(1);
+    } else {
+        p.seqlen_q = (int32_t)q.size(1);
+        p.q_batch_stride = q.stride(0);
+        p.q_row_stride = q.stride(1);
+        p.q_head_stride = q.stride(2);
+    }
     p.k = kcache.data_ptr();
     p.k_batch_stride = kcache.stride(0);
     p.k_row_stride = kcache.stride(1);
@@ -123,7 +145,7 @@ std::tuple<Tensor, Tensor> fwd_kvcache(const Tensor& q, Tensor& kcache, Tensor& 
         p.max_blocks_per_seq = (int32_t)block_table->size(1);
         p.block_table_rows = (int32_t)block_table->size(0);
         p.page_block_size = (int32_t)kcache.size(1);
-        const int64_t rows_needed = cache_batch_idx.has_value() ? 1 : q.size(0);
+        const int64_t rows_needed = cache_batch_idx.has_value() ? 1 : batch;
         TORCH_CHECK(block_table->size(0) >= rows_needed, "block_table must have a row per batch entry");
     }
     Tensor kn, vn;
@@ -136,28 +158,45 @@ std::tuple<Tensor, Tensor> fwd_kvcache(const Tensor& q, Tensor& kcache, Tensor& 
         check_dev(vn, q, "v");
         TORCH_CHECK(kn.scalar_type() == q.scalar_type() && vn.scalar_type() == q.scalar_type(),
                     "Key and value must have the same dtype as query");
-        TORCH_CHECK(kn.dim() == 4 && kn.size(0) == q.size(0) && kn.size(2) == p.nheads_k && kn.size(3) == p.headdim,
-                    "k must have shape (batch_size, seqlen_new, num_heads_k, head_size)");
         TORCH_CHECK(vn.sizes() == kn.sizes(), "v must have the same shape as k");
         p.k_new = kn.data_ptr();
-        p.knew_batch_stride = kn.stride(0);
-        p.knew_row_stride = kn.stride(1);
-        p.knew_head_stride = kn.stride(2);
         p.v_new = vn.data_ptr();
-        p.vnew_batch_stride = vn.stride(0);
-        p.vnew_row_stride = vn.stride(1);
-        p.vnew_head_stride = vn.stride(2);
-        p.seqlen_new = (int32_t)kn.size(1);
+        if (cu_seqlens_k_new.has_value()) {
+            TORCH_CHECK(kn.dim() == 3 && kn.size(1) == p.nheads_k && kn.size(2) == p.headdim,
+                        "k must have shape (total_k_new, num_heads_k, head_size) with cu_seqlens_k_new");
+            TORCH_CHECK(cu_seqlens_k_new->numel() == batch + 1, "cu_seqlens_k_new must have shape (batch_size + 1)");
+            p.cu_seqlens_k_new = i32_ptr(cu_seqlens_k_new, q, "cu_seqlens_k_new");
+            p.total_k_new = (int32_t)kn.size(0);
+            p.knew_row_stride = kn.stride(0);
+            p.knew_head_stride = kn.stride(1);
+            p.vnew_row_stride = vn.stride(0);
+            p.vnew_head_stride = vn.stride(1);
+        } else {
+            TORCH_CHECK(kn.dim() == 4 && kn.size(0) == batch && kn.size(2) == p.nheads_k && kn.size(3) == p.headdim,
+                        "k must have shape (batch_size, seqlen_new, num_heads_k, head_size)");
+            p.knew_batch_stride = kn.stride(0);
+            p.knew_row_stride = kn.stride(1);
+            p.knew_head_stride = kn.stride(2);
+            p.vnew_batch_stride = vn.stride(0);
+            p.vnew_row_stride = vn.stride(1);
+            p.vnew_head_stride = vn.stride(2);
+            p.seqlen_new = (int32_t)kn.size(1);
+        }
     } else {
         TORCH_CHECK(!v_new.has_value(), "If value is supplied, key must also be passed in");
+        TORCH_CHECK(!cu_seqlens_k_new.has_value(), "cu_seqlens_k_new is given without new keys k / v");
     }
-    if (seqlens_k.has_value()) {
-        p.cache_seqlens = i32_ptr(seqlens_k, q, "seqlens_k");
-        TORCH_CHECK(seqlens_k->numel() == q.size(0), "seqlens_k must have shape (batch_size)");
-    }
-    if (cache_batch_idx.has_value()) {
-        p.cache_batch_idx = i32_ptr(cache_batch_idx, q, "cache_batch_idx");
-        TORCH_CHECK(cache_batch_idx->numel() == q.size(0), "cache_batch_idx must have shape (batch_size)");
+    auto per_batch = [&](const OptT& t, const char* name) -> const int32_t* {
+        if (!t.has_value()) return nullptr;
+        TORCH_CHECK(t->numel() == batch, name, " must have shape (batch_size)");
+        return i32_ptr(t, q, name);
+    };
+    p.cache_seqlens = per_batch(seqlens_k, "seqlens_k");
+    p.cache_batch_idx = per_batch(cache_batch_idx, "cache_batch_idx");
+    p.cache_leftpad = per_batch(leftpad_k, "cache_leftpad");
+    p.rotary_seqlens = per_batch(rotary_seqlens, "rotary_seqlens");
+    if (leftpad_k.has_value()) {
+        TORCH_CHECK(seqlens_k.has_value(), "cache_leftpad needs cache_seqlens");
     }
     if (rotary_cos.has_value()) {
         TORCH_CHECK(rotary_sin.has_value(), "rotary_sin must be given with rotary_cos");
@@ -174,17 +213,25 @@ std::tuple<Tensor, Tensor> fwd_kvcache(const Tensor& q, Tensor& kcache, Tensor& 
         p.seqlen_ro = (int32_t)rotary_cos->size(0);
         p.rotary_interleaved = is_rotary_interleaved ? 1 : 0;
     }
-    set_alibi(p, alibi_slopes, q, q.size(0), q.size(2));
+    set_alibi(p, alibi_slopes, q, batch, p.nheads);
     p.softmax_scale = (float)softmax_scale;
     p.softcap = (float)softcap;
     set_window(p, is_causal, window_size_left, window_size_right);
+    p.attention_chunk = (int32_t)attention_chunk;
     p.num_splits = (int32_t)num_splits;
     Tensor out = at::empty(q.sizes(), q.options());
-    Tensor lse = at::empty({q.size(0), q.size(2), q.size(1)}, q.options().dtype(at::kFloat));
+    Tensor lse = ragged_q ? at::empty({q.size(1), q.size(0)}, q.options().dtype(at::kFloat))
+                          : at::empty({q.size(0), q.size(2), q.size(1)}, q.options().dtype(at::kFloat));
     p.out = out.data_ptr();
-    p.out_batch_stride = out.stride(0);
-    p.out_row_stride = out.stride(1);
-    p.out_head_stride = out.stride(2);
+    if (ragged_q) {
+        p.out_batch_stride = 0;
+        p.out_row_stride = out.stride(0);
+        p.out_head_stride = out.stride(1);
+    } else {
+        p.out_batch_stride = out.stride(0);
+        p.out_row_stride = out.stride(1);
+        p.out_head_stride = out.stride(2);
+    }
     p.softmax_lse = lse.data_ptr<float>();
     Tensor ws = workspace_for(p, FA_KIND_KVCACHE, q);
     p.workspace = ws.data_ptr();
@@ -193,10 +240,38 @@ std::tuple<Tensor, Tensor> fwd_kvcache(const Tensor& q, Tensor& kcache, Tensor& 
     return {out, lse};
 }
 
+std::tuple<Tensor, Tensor> fwd_kvcache(const Tensor& q, Tensor& kcache, Tensor& vcache, const OptT& k_new,
+                                       const OptT& v_new, const OptT& seqlens_k, const OptT& rotary_cos,
+                                       const OptT& rotary_sin, const OptT& cache_batch_idx, const OptT& leftpad_k,
+                                       const OptT& block_table, const OptT& alibi_slopes, double softmax_scale,
+                                       bool is_causal, int64_t window_size_left, int64_t window_size_right,
+                                       double softcap, bool is_rotary_interleaved, int64_t num_splits) {
+    return kvcache_impl(q, kcache, vcache, k_new, v_new, seqlens_k, rotary_cos, rotary_sin, cache_batch_idx,
+                        leftpad_k, block_table, alibi_slopes, std::nullopt, std::nullopt, 0, std::nullopt,
+                        softmax_scale, is_causal, window_size_left, window_size_right, 0, softcap,
+                        is_rotary_interleaved, num_splits);
+}
+
+std::tuple<Tensor, Tensor> fwd_kvcache_v3(const Tensor& q, Tensor& kcache, Tensor& vcache, const OptT& k_new,
+                                          const OptT& v_new, const OptT& seqlens_k, const OptT& rotary_cos,
+                                          const OptT& rotary_sin, const OptT& cache_batch_idx,
+                                          const OptT& leftpad_k, const OptT& block_table,
+                                          const OptT& alibi_slopes, const OptT& cu_seqlens_q,
+                                          const OptT& cu_seqlens_k_new, int64_t max_seqlen_q,
+                                          const OptT& rotary_seqlens, double softmax_scale, bool is_causal,
+                                          int64_t window_size_left, int64_t window_size_right,
+                                          int64_t attention_chunk, double softcap, bool is_rotary_interleaved,
+                                          int64_t num_splits) {
+    return kvcache_impl(q, kcache, vcache, k_new, v_new, seqlens_k, rotary_cos, rotary_sin, cache_batch_idx,
+                        leftpad_k, block_table, alibi_slopes, cu_seqlens_q, cu_seqlens_k_new, max_seqlen_q,
+                        rotary_seqlens, softmax_scale, is_causal, window_size_left, window_size_right,
+                        attention_chunk, softcap, is_rotary_interleaved, num_splits);
+}
+
 // ---- flash_attn_func ------------------------------------------------------------------------
 std::tuple<Tensor, Tensor> fwd(const Tensor& q, const Tensor& k, const Tensor& v, const OptT& alibi_slopes,
                                double p_dropout, double softmax_scale, bool is_causal, int64_t window_size_left,
-                               int64_t window_size_right, double softcap) {
+                               int64_t window_size_right, double softcap, int64_t attention_chunk) {
     c10::DeviceGuard guard(q.device());
     TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
     check_dev(k, q, "k");
@@ -237,6 +312,7 @@ std::tuple<Tensor, Tensor> fwd(const Tensor& q, const Tensor& k, const Tensor& v
     p.softmax_scale = (float)softmax_scale;
     p.softcap = (float)softcap;
     set_window(p, is_causal, window_size_left, window_size_right);
+    p.attention_chunk = (int32_t)attention_chunk;
     p.num_splits = 0;
     Tensor out = at::empty(q.sizes(), q.options());
     Tensor lse = at::empty({q.size(0), q.size(2), q.size(1)}, q.options().dtype(at::kFloat));
@@ -258,7 +334,7 @@ std::tuple<Tensor, Tensor> varlen_fwd(const Tensor& q, const Tensor& k, const Te
                                       const OptT& alibi_slopes,
                                       int64_t max_seqlen_q, int64_t max_seqlen_k, double p_dropout,
                                       double softmax_scale, bool is_causal, int64_t window_size_left,
-                                      int64_t window_size_right, double softcap) {
+                                      int64_t window_size_right, double softcap, int64_t attention_chunk) {
     c10::DeviceGuard guard(q.device());
     TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
     check_dev(k, q, "k");
@@ -324,6 +400,7 @@ std::tuple<Tensor, Tensor> varlen_fwd(const Tensor& q, const Tensor& k, const Te
     p.softmax_scale = (float)softmax_scale;
     p.softcap = (float)softcap;
     set_window(p, is_causal, window_size_left, window_size_right);
+    p.attention_chunk = (int32_t)attention_chunk;
     p.num_splits = 0;
     Tensor out = at::empty(q.sizes(), q.options());
     Tensor lse = at::empty({q.size(1), q.size(0)}, q.options().dtype(at::kFloat));
@@ -395,7 +472,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> bwd(const Tensor& dout, const Tensor&
                                                const Tensor& out, const Tensor& softmax_lse, const OptT& alibi_slopes,
                                                double p_dropout, double softmax_scale, bool is_causal,
                                                int64_t window_size_left, int64_t window_size_right, double softcap,
-                                               bool deterministic) {
+                                               bool deterministic, int64_t attention_chunk) {
     c10::DeviceGuard guard(q.device());
     fa_bwd_params p{};
     set_bwd_common(p, dout, q, k, v, out, softmax_lse);
@@ -454,6 +531,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> bwd(const Tensor& dout, const Tensor&
     p.window_size_left = (int32_t)window_size_left;
     p.window_size_right = (int32_t)window_size_right;
     p.deterministic = deterministic ? 1 : 0;
+    p.attention_chunk = (int32_t)attention_chunk;
     check_status(fa_mha_bwd(&p, cur_stream()));
     return {dq, dk, dv, sd};
 }
@@ -464,7 +542,8 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> varlen_bwd(const Tensor& dout, const 
                                                       const OptT& alibi_slopes, int64_t max_seqlen_q,
                                                       int64_t max_seqlen_k, double p_dropout, double softmax_scale,
                                                       bool is_causal, int64_t window_size_left,
-                                                      int64_t window_size_right, double softcap, bool deterministic) {
+                                                      int64_t window_size_right, double softcap, bool deterministic,
+                                                      int64_t attention_chunk) {
     c10::DeviceGuard guard(q.device());
     fa_bwd_params p{};
     set_bwd_common(p, dout, q, k, v, out, softmax_lse);
@@ -528,6 +607,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> varlen_bwd(const Tensor& dout, const 
     p.window_size_left = (int32_t)window_size_left;
     p.window_size_right = (int32_t)window_size_right;
     p.deterministic = deterministic ? 1 : 0;
+    p.attention_chunk = (int32_t)attention_chunk;
     check_status(fa_mha_varlen_bwd(&p, cur_stream()));
     return {dq, dk, dv, sd};
 }
@@ -542,26 +622,34 @@ TORCH_LIBRARY(fa_mi355x, m) {
         "float softcap, bool is_rotary_interleaved, int num_splits) -> (Tensor, Tensor)");
     m.def(
         "fwd(Tensor q, Tensor k, Tensor v, Tensor? alibi_slopes, float p_dropout, float softmax_scale, bool is_causal, "
-        "int window_size_left, int window_size_right, float softcap) -> (Tensor, Tensor)");
+        "int window_size_left, int window_size_right, float softcap, int attention_chunk=0) -> (Tensor, Tensor)");
+    m.def(
+        "fwd_kvcache_v3(Tensor q, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor? k, Tensor? v, Tensor? seqlens_k, "
+        "Tensor? rotary_cos, Tensor? rotary_sin, Tensor? cache_batch_idx, Tensor? leftpad_k, Tensor? block_table, "
+        "Tensor? alibi_slopes, Tensor? cu_seqlens_q, Tensor? cu_seqlens_k_new, int max_seqlen_q, "
+        "Tensor? rotary_seqlens, float softmax_scale, bool is_causal, int window_size_left, int window_size_right, "
+        "int attention_chunk, float softcap, bool is_rotary_interleaved, int num_splits) -> (Tensor, Tensor)");
     m.def(
         "varlen_fwd(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor? cu_seqlens_k, Tensor? seqused_k, "
         "Tensor? block_table, "
         "Tensor? alibi_slopes, int max_seqlen_q, int max_seqlen_k, float p_dropout, float softmax_scale, "
-        "bool is_causal, int window_size_left, int window_size_right, float softcap) -> (Tensor, Tensor)");
+        "bool is_causal, int window_size_left, int window_size_right, float softcap, int attention_chunk=0) "
+        "-> (Tensor, Tensor)");
     m.def("fwd_combine(Tensor out_partial, Tensor lse_partial, Tensor? out, ScalarType? out_dtype) -> (Tensor, Tensor)");
     m.def(
         "bwd(Tensor dout, Tensor q, Tensor k, Tensor v, Tensor out, Tensor softmax_lse, Tensor? alibi_slopes, "
         "float p_dropout, float softmax_scale, bool is_causal, int window_size_left, int window_size_right, "
-        "float softcap, bool deterministic) -> (Tensor, Tensor, Tensor, Tensor)");
+        "float softcap, bool deterministic, int attention_chunk=0) -> (Tensor, Tensor, Tensor, Tensor)");
     m.def(
         "varlen_bwd(Tensor dout, Tensor q, Tensor k, Tensor v, Tensor out, Tensor softmax_lse, Tensor cu_seqlens_q, "
         "Tensor cu_seqlens_k, Tensor? alibi_slopes, int max_seqlen_q, int max_seqlen_k, float p_dropout, "
         "float softmax_scale, bool is_causal, int window_size_left, int window_size_right, float softcap, "
-        "bool deterministic) -> (Tensor, Tensor, Tensor, Tensor)");
+        "bool deterministic, int attention_chunk=0) -> (Tensor, Tensor, Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(fa_mi355x, CUDA, m) {
     m.impl("fwd_kvcache", &fwd_kvcache);
+    m.impl("fwd_kvcache_v3", &fwd_kvcache_v3);
     m.impl("fwd", &fwd);
     m.impl("varlen_fwd", &varlen_fwd);
     m.impl("fwd_combine", &fwd_combine);

@@ -14,16 +14,29 @@ def _fwd_kvcache_fake(q, k_cache, v_cache, k, v, seqlens_k, rotary_cos, rotary_s
     return torch.empty_like(q), q.new_empty((b, h, sq), dtype=torch.float32)
 
 
+@torch.library.register_fake("fa_mi355x::fwd_kvcache_v3")
+def _fwd_kvcache_v3_fake(q, k_cache, v_cache, k, v, seqlens_k, rotary_cos, rotary_sin, cache_batch_idx, leftpad_k,
+                         block_table, alibi_slopes, cu_seqlens_q, cu_seqlens_k_new, max_seqlen_q, rotary_seqlens,
+                         softmax_scale, is_causal, window_size_left, window_size_right, attention_chunk, softcap,
+                         is_rotary_interleaved, num_splits):
+    if cu_seqlens_q is not None:
+        t, h, _ = q.shape
+        return torch.empty_like(q), q.new_empty((h, t), dtype=torch.float32)
+    b, sq, h, _ = q.shape
+    return torch.empty_like(q), q.new_empty((b, h, sq), dtype=torch.float32)
+
+
 @torch.library.register_fake("fa_mi355x::fwd")
 def _fwd_fake(q, k, v, alibi_slopes, p_dropout, softmax_scale, is_causal, window_size_left, window_size_right,
-              softcap):
+              softcap, attention_chunk=0):
     b, sq, h, _ = q.shape
     return torch.empty_like(q), q.new_empty((b, h, sq), dtype=torch.float32)
 
 
 @torch.library.register_fake("fa_mi355x::varlen_fwd")
 def _varlen_fwd_fake(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, block_table, alibi_slopes, max_seqlen_q, max_seqlen_k,
-                     p_dropout, softmax_scale, is_causal, window_size_left, window_size_right, softcap):
+                     p_dropout, softmax_scale, is_causal, window_size_left, window_size_right, softcap,
+                     attention_chunk=0):
     t, h, _ = q.shape
     return torch.empty_like(q), q.new_empty((h, t), dtype=torch.float32)
 
@@ -37,7 +50,7 @@ def _fwd_combine_fake(out_partial, lse_partial, out, out_dtype):
 
 @torch.library.register_fake("fa_mi355x::bwd")
 def _bwd_fake(dout, q, k, v, out, softmax_lse, alibi_slopes, p_dropout, softmax_scale, is_causal, window_size_left,
-              window_size_right, softcap, deterministic):
+              window_size_right, softcap, deterministic, attention_chunk=0):
     b, sq, h, _ = q.shape
     return (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
             q.new_empty((b, h, sq), dtype=torch.float32))
@@ -46,7 +59,7 @@ def _bwd_fake(dout, q, k, v, out, softmax_lse, alibi_slopes, p_dropout, softmax_
 @torch.library.register_fake("fa_mi355x::varlen_bwd")
 def _varlen_bwd_fake(dout, q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k, alibi_slopes, max_seqlen_q,
                      max_seqlen_k, p_dropout, softmax_scale, is_causal, window_size_left, window_size_right, softcap,
-                     deterministic):
+                     deterministic, attention_chunk=0):
     t, h, _ = q.shape
     return (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
             q.new_empty((h, t), dtype=torch.float32))

@@ -11,7 +11,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 CORE_LIB = os.path.join(_HERE, "lib", "libfa_mi355x.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 FA_OK, FA_EINVAL, FA_EUNSUPPORTED, FA_EHIP, FA_EWORKSPACE = 0, 1, 2, 3, 4
 FA_DTYPE_FP16, FA_DTYPE_BF16, FA_DTYPE_FP32 = 0, 1, 2
 FA_KIND_KVCACHE, FA_KIND_DENSE, FA_KIND_VARLEN = 0, 1, 2
@@ -48,6 +48,8 @@ class FwdParams(ctypes.Structure):
         ("is_causal", _i32), ("window_size_left", _i32), ("window_size_right", _i32), ("num_splits", _i32),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("stage_events", _vp),
+        ("cache_leftpad", _vp), ("cu_seqlens_k_new", _vp), ("total_k_new", _i32), ("rotary_seqlens", _vp),
+        ("attention_chunk", _i32),
     ]
 
 
@@ -70,6 +72,7 @@ class BwdParams(ctypes.Structure):
         ("softmax_scale", ctypes.c_float), ("softcap", ctypes.c_float), ("dropout_p", ctypes.c_float),
         ("is_causal", _i32), ("window_size_left", _i32), ("window_size_right", _i32), ("deterministic", _i32),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("attention_chunk", _i32),
     ]
 
 

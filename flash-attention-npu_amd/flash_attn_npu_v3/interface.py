@@ -49,13 +49,13 @@ class FlashAttnFunc(torch.autograd.Function):
     def forward(ctx, q, k, v, softmax_scale, causal, qv=None, q_descale=None, k_descale=None, v_descale=None,
                 window_size=(-1, -1), attention_chunk=0, softcap=0.0, num_splits=1, pack_gqa=None,
                 deterministic=False, sm_margin=0, return_softmax=False, scheduler_metadata=None):
-        _reject(qv=qv, q_descale=q_descale, k_descale=k_descale, v_descale=v_descale, attention_chunk=attention_chunk)
+        _reject(qv=qv, q_descale=q_descale, k_descale=k_descale, v_descale=v_descale)
         if softmax_scale is None:
             softmax_scale = q.shape[-1] ** (-0.5)
         _check_metadata(scheduler_metadata, q.device)
         q, k, v = [maybe_contiguous(x) for x in (q, k, v)]
         out, softmax_lse = ops.fwd(q, k, v, None, 0.0, float(softmax_scale), bool(causal), int(window_size[0]),
-                                   int(window_size[1]), float(softcap))
+                                   int(window_size[1]), float(softcap), int(attention_chunk))
         if any(x.requires_grad for x in (q, k, v)):
             ctx.save_for_backward(q, k, v, out, softmax_lse)
             ctx.softmax_scale = softmax_scale
@@ -63,6 +63,7 @@ class FlashAttnFunc(torch.autograd.Function):
             ctx.window_size = window_size
             ctx.softcap = softcap
             ctx.deterministic = deterministic
+            ctx.attention_chunk = attention_chunk
         return (out, softmax_lse) if return_softmax else out
 
     @staticmethod
@@ -70,7 +71,8 @@ class FlashAttnFunc(torch.autograd.Function):
         q, k, v, out, softmax_lse = ctx.saved_tensors
         dq, dk, dv, _ = ops.bwd(maybe_contiguous(dout), q, k, v, out, softmax_lse, None, 0.0,
                                 float(ctx.softmax_scale), bool(ctx.causal), int(ctx.window_size[0]),
-                                int(ctx.window_size[1]), float(ctx.softcap), bool(ctx.deterministic))
+                                int(ctx.window_size[1]), float(ctx.softcap), bool(ctx.deterministic),
+                                int(ctx.attention_chunk))
         return (dq, dk, dv) + (None,) * 15
 
 
@@ -80,15 +82,15 @@ class FlashAttnVarlenFunc(torch.autograd.Function):
                 softmax_scale, causal, qv=None, q_descale=None, k_descale=None, v_descale=None, window_size=(-1, -1),
                 attention_chunk=0, softcap=0.0, num_splits=1, pack_gqa=None, deterministic=False, sm_margin=0,
                 return_softmax=False, scheduler_metadata=None):
-        _reject(seqused_q=seqused_q, qv=qv, q_descale=q_descale, k_descale=k_descale, v_descale=v_descale,
-                attention_chunk=attention_chunk)
+        _reject(seqused_q=seqused_q, qv=qv, q_descale=q_descale, k_descale=k_descale, v_descale=v_descale)
         if softmax_scale is None:
             softmax_scale = q.shape[-1] ** (-0.5)
         _check_metadata(scheduler_metadata, q.device)
         q, k, v = [maybe_contiguous(x) for x in (q, k, v)]
         out, softmax_lse = ops.varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, None, None,
                                           int(max_seqlen_q), int(max_seqlen_k), 0.0, float(softmax_scale),
-                                          bool(causal), int(window_size[0]), int(window_size[1]), float(softcap))
+                                          bool(causal), int(window_size[0]), int(window_size[1]), float(softcap),
+                                          int(attention_chunk))
         if any(x.requires_grad for x in (q, k, v)):
             ctx.save_for_backward(q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k)
             ctx.has_seqused_k = seqused_k is not None
@@ -99,6 +101,7 @@ class FlashAttnVarlenFunc(torch.autograd.Function):
             ctx.window_size = window_size
             ctx.softcap = softcap
             ctx.deterministic = deterministic
+            ctx.attention_chunk = attention_chunk
         return (out, softmax_lse) if return_softmax else out
 
     @staticmethod
@@ -109,7 +112,8 @@ class FlashAttnVarlenFunc(torch.autograd.Function):
         dq, dk, dv, _ = ops.varlen_bwd(maybe_contiguous(dout), q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k,
                                        None, int(ctx.max_seqlen_q), int(ctx.max_seqlen_k), 0.0,
                                        float(ctx.softmax_scale), bool(ctx.causal), int(ctx.window_size[0]),
-                                       int(ctx.window_size[1]), float(ctx.softcap), bool(ctx.deterministic))
+                                       int(ctx.window_size[1]), float(ctx.softcap), bool(ctx.deterministic),
+                                       int(ctx.attention_chunk))
         return (dq, dk, dv) + (None,) * 21
 
 
@@ -161,41 +165,52 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None, rotary
     seqlen_cache, nheads_k, headdim), (num_blocks, page_block_size, nheads_k,
     headdim) with page_table, or with cu_seqlens_q and no page_table a packed
     (total_k, nheads_k, headdim) cache indexed by the prefix sums of
-    cache_seqlens. Returns out, or (out, softmax_lse, out_accum, lse_accum)
-    when return_softmax_lse (the accumulators are empty tensors)."""
+    cache_seqlens. k / v (appended in place at cache_seqlens) are (batch_size,
+    seqlen_new, nheads_k, headdim), or (total_k_new, nheads_k, headdim) split
+    by cu_seqlens_k_new. cache_leftpad[b] is the first valid cache row of
+    sequence b (contiguous caches). Rotary positions start at rotary_seqlens[b]
+    (default cache_seqlens[b]). attention_chunk > 0 restricts each query to
+    the keys of its own chunk of that size. Returns out, or (out, softmax_lse,
+    out_accum, lse_accum) when return_softmax_lse (the accumulators are empty
+    tensors)."""
     assert k_cache.stride(-1) == 1, "k_cache must have contiguous last dimension"
     assert v_cache.stride(-1) == 1, "v_cache must have contiguous last dimension"
-    _reject(qv=qv, cache_leftpad=cache_leftpad, cu_seqlens_k_new=cu_seqlens_k_new, rotary_seqlens=rotary_seqlens,
-            q_descale=q_descale, k_descale=k_descale, v_descale=v_descale, attention_chunk=attention_chunk)
+    _reject(qv=qv, q_descale=q_descale, k_descale=k_descale, v_descale=v_descale)
     if softmax_scale is None:
         softmax_scale = q.shape[-1] ** (-0.5)
+    batch = q.shape[0] if cu_seqlens_q is None else cu_seqlens_q.numel() - 1
     if cache_seqlens is not None and isinstance(cache_seqlens, int):
-        batch = q.shape[0] if cu_seqlens_q is None else cu_seqlens_q.numel() - 1
         cache_seqlens = torch.full((batch,), cache_seqlens, dtype=torch.int32, device=k_cache.device)
     cache_seqlens = maybe_contiguous(cache_seqlens)
     _check_metadata(scheduler_metadata, q.device)
     q, k, v = [maybe_contiguous(x) for x in (q, k, v)]
-    if cu_seqlens_q is None:
-        out, softmax_lse = ops.fwd_kvcache(q, k_cache, v_cache, k, v, cache_seqlens, rotary_cos, rotary_sin,
-                                           maybe_contiguous(cache_batch_idx), None, maybe_contiguous(page_table),
-                                           None, float(softmax_scale), bool(causal), int(window_size[0]),
-                                           int(window_size[1]), float(softcap), bool(rotary_interleaved),
-                                           int(num_splits))
-    else:
-        # varlen (TND) queries against the cache: per-sequence key counts come
-        # from cache_seqlens; a contiguous cache is packed by their prefix sums
-        # (csrc/arch22/flash_attn_npu_v3/flash_api.cpp:431-441 in the reference).
-        _reject(k=k, v=v, rotary_cos=rotary_cos, cache_batch_idx=cache_batch_idx)
+    if cu_seqlens_q is not None and max_seqlen_q is None:
+        raise RuntimeError("max_seqlen_q is required with cu_seqlens_q")
+    if cu_seqlens_q is not None and page_table is None and k_cache.dim() == 3:
+        # varlen (TND) queries against a packed (total_k, nheads_k, headdim)
+        # cache indexed by the prefix sums of cache_seqlens
+        # (csrc/arch22/flash_attn_npu_v3/flash_api.cpp:431-441 in the reference)
+        _reject(k=k, v=v, rotary_cos=rotary_cos, cache_batch_idx=cache_batch_idx, cache_leftpad=cache_leftpad,
+                cu_seqlens_k_new=cu_seqlens_k_new)
         if cache_seqlens is None:
             raise RuntimeError("cache_seqlens is required with cu_seqlens_q")
-        if max_seqlen_q is None:
-            raise RuntimeError("max_seqlen_q is required with cu_seqlens_q")
-        cu_k = None if page_table is not None else _cu_from_lengths(cache_seqlens)
-        max_k = (page_table.shape[1] * k_cache.shape[1]) if page_table is not None else k_cache.shape[0]
-        out, softmax_lse = ops.varlen_fwd(q, k_cache, v_cache, cu_seqlens_q, cu_k, cache_seqlens,
-                                          maybe_contiguous(page_table), None, int(max_seqlen_q), int(max_k), 0.0,
-                                          float(softmax_scale), bool(causal), int(window_size[0]),
-                                          int(window_size[1]), float(softcap))
+        cu_k = _cu_from_lengths(cache_seqlens)
+        out, softmax_lse = ops.varlen_fwd(q, k_cache, v_cache, cu_seqlens_q, cu_k, cache_seqlens, None, None,
+                                          int(max_seqlen_q), int(k_cache.shape[0]), 0.0, float(softmax_scale),
+                                          bool(causal), int(window_size[0]), int(window_size[1]), float(softcap),
+                                          int(attention_chunk))
+    else:
+        # (batch, seqlen) or ragged (total_q) queries against a (batch_cache,
+        # seqlen_cache) or paged cache, with the in-place append of k / v
+        # (ragged with cu_seqlens_k_new), rotary at rotary_seqlens (default
+        # cache_seqlens), cache_leftpad and attention_chunk
+        out, softmax_lse = ops.fwd_kvcache_v3(q, k_cache, v_cache, k, v, cache_seqlens, rotary_cos, rotary_sin,
+                                              maybe_contiguous(cache_batch_idx), maybe_contiguous(cache_leftpad),
+                                              maybe_contiguous(page_table), None, cu_seqlens_q, cu_seqlens_k_new,
+                                              int(max_seqlen_q or 0), maybe_contiguous(rotary_seqlens),
+                                              float(softmax_scale), bool(causal), int(window_size[0]),
+                                              int(window_size[1]), int(attention_chunk), float(softcap),
+                                              bool(rotary_interleaved), int(num_splits))
     if return_softmax_lse:
         oa, la = _empty_accum(out)
         return out, softmax_lse, oa, la

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define FA_MI355X_ABI_VERSION 1
+#define FA_MI355X_ABI_VERSION 2
 
 typedef enum {
     FA_OK = 0,
@@ -132,6 +132,23 @@ typedef struct fa_fwd_params {
        `stream` before the KV append, before the attention kernel, before the
        split-KV combine and after the last kernel of the call. */
     void* const* stage_events;
+
+    /* ---- kvcache extensions of the v3 API (all optional: NULL / 0 = off) ----
+       The reference rejects these arguments (csrc/arch22/flash_attn_npu_v3/
+       flash_api.cpp:150-162, v2 flash_api.cpp:416); the semantics are the
+       flash_attn_with_kvcache docstring's (README.md:311-401 of the reference).
+       The kvcache forward also takes cu_seqlens_q / total_q (above): q and out
+       are then (total_q, H, D) and softmax_lse is (H, total_q). */
+    const int32_t* cache_leftpad;    /* (B,): first valid row of each sequence's cache (contiguous caches);
+                                        keys are cache rows [leftpad, cache_seqlens + new) */
+    const int32_t* cu_seqlens_k_new; /* (B+1,): k_new / v_new are (total_k_new, Hk, D) and sequence b
+                                        appends cu[b+1] - cu[b] tokens */
+    int32_t total_k_new;             /* rows of k_new / v_new with cu_seqlens_k_new */
+    const int32_t* rotary_seqlens;   /* (B,): rotary position of the first new token / query
+                                        (default cache_seqlens) */
+    int32_t attention_chunk;         /* > 0: a query sees only keys of its own chunk
+                                        [c*floor(p/c), c*floor(p/c) + c) of its diagonal position p,
+                                        intersected with the causal / local window */
 } fa_fwd_params;
 
 /* Library / ABI version. */
@@ -207,6 +224,8 @@ typedef struct fa_bwd_params {
 
     void* workspace;                /* unused: fa_bwd_workspace_size reports 0 */
     size_t workspace_bytes;
+
+    int32_t attention_chunk;        /* as in fa_fwd_params: 0 = off */
 } fa_bwd_params;
 
 /* Host-only validation of a backward call (kind: FA_KIND_DENSE or FA_KIND_VARLEN). */

@@ -35,8 +35,9 @@ def _window(sq, sk, causal, wl, wr):
     return wl, wr
 
 
-def _visible(sq, sk, causal, wl, wr):
-    """Keep-mask (Sq, Sk): bottom-right aligned causal / local window."""
+def _visible(sq, sk, causal, wl, wr, chunk=0):
+    """Keep-mask (Sq, Sk): bottom-right aligned causal / local window and, with
+    attention_chunk c > 0 (v3 API), keys in [c*floor(d/c), c*floor(d/c) + c)."""
     wl, wr = _window(sq, sk, causal, wl, wr)
     i = np.arange(sq)[:, None]
     j = np.arange(sk)[None, :]
@@ -46,10 +47,13 @@ def _visible(sq, sk, causal, wl, wr):
         keep &= j <= d + wr
     if wl >= 0:
         keep &= j >= d - wl
+    if chunk > 0:
+        c0 = np.floor_divide(d, chunk) * chunk
+        keep &= (j >= c0) & (j < c0 + chunk)
     return keep
 
 
-def _one(q, k, v, do, lse, *, scale, softcap, causal, window, alibi_row):
+def _one(q, k, v, do, lse, *, scale, softcap, causal, window, alibi_row, chunk=0):
     """One sequence. q, do: (H, Sq, D); k, v: (Hk, Sk, D); lse: (H, Sq).
     Returns dq (H, Sq, D), dk, dv (Hk, Sk, D)."""
     H, sq, _ = q.shape
@@ -67,7 +71,7 @@ def _one(q, k, v, do, lse, *, scale, softcap, causal, window, alibi_row):
         j = np.arange(sk)[None, :]
         dist = np.abs(i + sk - sq - j).astype(np.float64)
         s = s - alibi_row[:, None, None] * dist[None]
-    keep = _visible(sq, sk, causal, *window)
+    keep = _visible(sq, sk, causal, *window, chunk=chunk)
     with np.errstate(invalid="ignore", over="ignore"):
         p = np.exp(s - lse[:, :, None])
     p = np.where(keep[None], p, 0.0)
@@ -85,7 +89,7 @@ def _one(q, k, v, do, lse, *, scale, softcap, causal, window, alibi_row):
 
 
 def attention_bwd(q, k, v, dout, lse, *, scale, softcap=0.0, causal=False, window=(-1, -1), alibi=None,
-                  cu_seqlens_q=None, cu_seqlens_k=None):
+                  cu_seqlens_q=None, cu_seqlens_k=None, chunk=0):
     """Gradients of the forward attention given its LSE.
 
     Dense: q, dout (B, Sq, H, D); k, v (B, Sk, Hk, D); lse (B, H, Sq).
@@ -107,7 +111,7 @@ def attention_bwd(q, k, v, dout, lse, *, scale, softcap=0.0, causal=False, windo
                 b if np.ndim(alibi) == 2 else 0]
             a, bk, c = _one(q[b].transpose(1, 0, 2), k[b].transpose(1, 0, 2), v[b].transpose(1, 0, 2),
                             dout[b].transpose(1, 0, 2), lse[b], scale=scale, softcap=softcap, causal=causal,
-                            window=window, alibi_row=ar)
+                            window=window, alibi_row=ar, chunk=chunk)
             dq[b] = a.transpose(1, 0, 2)
             dk[b] = bk.transpose(1, 0, 2)
             dv[b] = c.transpose(1, 0, 2)
@@ -122,7 +126,7 @@ def attention_bwd(q, k, v, dout, lse, *, scale, softcap=0.0, causal=False, windo
             b if np.ndim(alibi) == 2 else 0]
         a, bk, c = _one(q[qs:qe].transpose(1, 0, 2), k[ks:ke].transpose(1, 0, 2), v[ks:ke].transpose(1, 0, 2),
                         dout[qs:qe].transpose(1, 0, 2), lse[:, qs:qe], scale=scale, softcap=softcap,
-                        causal=causal, window=window, alibi_row=ar)
+                        causal=causal, window=window, alibi_row=ar, chunk=chunk)
         dq[qs:qe] = a.transpose(1, 0, 2)
         dk[ks:ke] += bk.transpose(1, 0, 2)
         dv[ks:ke] += c.transpose(1, 0, 2)

@@ -133,11 +133,17 @@ void orc_normalize_window(int seqlen_q, int seqlen_k, int causal, int* wl, int* 
     if (causal) *wr = 0;
 }
 
-static inline int key_visible(int i, int j, int sq, int sk, int wl, int wr) {
+/* attention_chunk c > 0 (v3 API, README.md:311-401; the reference rejects it):
+ * query i also needs j in [c*floor(d/c), c*floor(d/c) + c), d its diagonal key. */
+static inline int key_visible(int i, int j, int sq, int sk, int wl, int wr, int chunk) {
     long d = (long)i + sk - sq; /* diagonal key for query i (bottom-right aligned) */
     if (j < 0 || j >= sk) return 0;
     if (wl >= 0 && j < d - wl) return 0;
     if (wr >= 0 && j > d + wr) return 0;
+    if (chunk > 0) {
+        long c0 = (long)floor((double)d / (double)chunk) * chunk;
+        if (j < c0 || j >= c0 + chunk) return 0;
+    }
     return 1;
 }
 
@@ -182,7 +188,7 @@ static void attention_row(const orc_fwd_params* p, int b, int i, int h, int sq, 
         float lm = -INFINITY;
         for (int t = 0; t < n; t++) {
             int j = j0 + t;
-            if (!key_visible(i, j, sq, sk, p->wl, p->wr)) { s[t] = -INFINITY; continue; }
+            if (!key_visible(i, j, sq, sk, p->wl, p->wr, p->chunk)) { s[t] = -INFINITY; continue; }
             const uint16_t* kr = key_row(p, b, j, hk, 0);
             float acc = 0.f;
             for (int d = 0; d < D; d++) acc += qf[d] * to_f32(dt, kr[d]);
@@ -328,8 +334,10 @@ int orc_kv_append(const orc_append_params* p) {
                     int Dw = which ? p->Dv : p->D;
                     memcpy(buf, src, sizeof(uint16_t) * Dw);
                     if (!which && p->cos) {
-                        const uint16_t* cr = p->cos + (int64_t)j * p->cs_stride;
-                        const uint16_t* sr = p->sin + (int64_t)j * p->cs_stride;
+                        /* rotary at rotary_seqlens[b] + t when given (v3), else at the slot */
+                        const int64_t pos = p->rot_pos ? (int64_t)p->rot_pos[b] + t : j;
+                        const uint16_t* cr = p->cos + pos * p->cs_stride;
+                        const uint16_t* sr = p->sin + pos * p->cs_stride;
                         rotate_vec(p->dtype, buf, Dw, p->rotary_dim, p->interleaved, cr, sr);
                     }
                     uint16_t* cache = which ? p->v_cache : p->k_cache;

@@ -28,6 +28,7 @@ typedef struct {
     uint16_t* out; int64_t o_sb, o_si, o_sh;
     float* lse; int64_t lse_sb, lse_sh;    /* (B,H,Sq) or, when varlen, (H,T) */
     int nthreads;
+    int chunk;                             /* attention_chunk, 0 = off */
 } orc_fwd_params;
 
 typedef struct {
@@ -44,6 +45,7 @@ typedef struct {
     const int32_t* seqlens; const int32_t* batch_idx;
     const int32_t* block_table; int64_t bt_stride; int page;
     const uint16_t* cos; const uint16_t* sin; int64_t cs_stride;
+    const int32_t* rot_pos;                /* rotary position of token 0 per batch; NULL = seqlens */
 } orc_append_params;
 
 float orc_bf16_to_f32(uint16_t h);

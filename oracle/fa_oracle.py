@@ -46,6 +46,7 @@ class _FwdParams(ctypes.Structure):
         ("out", _u16p), ("o_sb", _i64), ("o_si", _i64), ("o_sh", _i64),
         ("lse", _f32p), ("lse_sb", _i64), ("lse_sh", _i64),
         ("nthreads", ctypes.c_int),
+        ("chunk", ctypes.c_int),
     ]
 
 
@@ -69,6 +70,7 @@ class _AppendParams(ctypes.Structure):
         ("seqlens", _i32p), ("batch_idx", _i32p),
         ("block_table", _i32p), ("bt_stride", _i64), ("page", ctypes.c_int),
         ("cos", _u16p), ("sin", _u16p), ("cs_stride", _i64),
+        ("rot_pos", _i32p),
     ]
 
 
@@ -151,7 +153,7 @@ def normalize_window(seqlen_q, seqlen_k, causal, wl, wr):
 
 def attention(q, k, v, *, dtype, scale, softcap=0.0, causal=False, window=(-1, -1), alibi=None,
               seqlens_k=None, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=None,
-              block_table=None, batch_idx=None, nthreads=1):
+              block_table=None, batch_idx=None, nthreads=1, chunk=0):
     """Blockwise golden forward.
 
     q: (B, Sq, H, D) or, with cu_seqlens_q, (T, H, D) uint16 bits.
@@ -227,7 +229,7 @@ def attention(q, k, v, *, dtype, scale, softcap=0.0, causal=False, window=(-1, -
         scale=scale, softcap=softcap, wl=wl, wr=wr,
         out=_p(out, ctypes.c_uint16), o_sb=o_st[0], o_si=o_st[1], o_sh=o_st[2],
         lse=_p(lse, ctypes.c_float), lse_sb=lse_sb, lse_sh=lse_sh,
-        nthreads=nthreads,
+        nthreads=nthreads, chunk=int(chunk),
     )
     rc = lib().orc_attention(ctypes.byref(p))
     if rc != 0:
@@ -253,8 +255,10 @@ def rotary(x, cos, sin, seqlens, *, dtype, interleaved, same_pos=False):
 
 
 def kv_append(k_cache, v_cache, k_new, v_new, seqlens, *, dtype, batch_idx=None, block_table=None,
-              cos=None, sin=None, interleaved=True):
-    """In-place append (after rotary on k) into copies of the caches; returns them."""
+              cos=None, sin=None, interleaved=True, rot_pos=None):
+    """In-place append (after rotary on k) into copies of the caches; returns them.
+    Token t of batch b goes to slot seqlens[b] + t and is rotated at rot_pos[b] + t
+    (default: at its slot)."""
     kc = np.array(k_cache, dtype=np.uint16, copy=True, order="C")
     vc = np.array(v_cache, dtype=np.uint16, copy=True, order="C")
     kn = np.ascontiguousarray(k_new, dtype=np.uint16)
@@ -265,6 +269,7 @@ def kv_append(k_cache, v_cache, k_new, v_new, seqlens, *, dtype, batch_idx=None,
     if cos is not None:
         cos = np.ascontiguousarray(cos, dtype=np.uint16)
         sin = np.ascontiguousarray(sin, dtype=np.uint16)
+    rp = None if rot_pos is None else np.ascontiguousarray(rot_pos, dtype=np.int32)
     B, S_new, Hk, D = kn.shape
     nst = _st(kn)
     cst = _st(kc)
@@ -280,7 +285,8 @@ def kv_append(k_cache, v_cache, k_new, v_new, seqlens, *, dtype, batch_idx=None,
                       bt_stride=(bt.shape[1] if bt is not None else 0),
                       page=(kc.shape[1] if bt is not None else 0),
                       cos=_p(cos, ctypes.c_uint16), sin=_p(sin, ctypes.c_uint16),
-                      cs_stride=(cos.shape[1] if cos is not None else 0))
+                      cs_stride=(cos.shape[1] if cos is not None else 0),
+                      rot_pos=_p(rp, ctypes.c_int32))
     lib().orc_kv_append(ctypes.byref(p))
     return kc, vc
 
@@ -322,4 +328,85 @@ def kvcache_forward(q, k_cache, v_cache, *, dtype, cache_seqlens, k=None, v=None
     out, lse = attention(q, kc, vc, dtype=dtype, scale=softmax_scale, softcap=softcap, causal=causal,
                          window=window, alibi=alibi, seqlens_k=seqlens + s_new,
                          block_table=block_table, batch_idx=cache_batch_idx, nthreads=nthreads)
+    return out, lse, kc, vc
+
+
+def kvcache_forward_v3(q, k_cache, v_cache, *, dtype, cache_seqlens, k=None, v=None, rotary_cos=None,
+                       rotary_sin=None, rotary_interleaved=True, cache_batch_idx=None, block_table=None,
+                       softmax_scale=None, causal=False, window=(-1, -1), softcap=0.0, alibi=None,
+                       cache_leftpad=None, rotary_seqlens=None, cu_seqlens_q=None, max_seqlen_q=None,
+                       cu_seqlens_k_new=None, attention_chunk=0, nthreads=1):
+    """The v3 flash_attn_with_kvcache contract (README.md:311-401 of the
+    reference, whose kernels reject the extensions), one sequence at a time:
+
+      * q is (B, Sq, H, D), or (total_q, H, D) split by cu_seqlens_q;
+      * k / v are (B, S_new, Hk, D), or (total_k_new, Hk, D) split by
+        cu_seqlens_k_new; token t of sequence b is appended at slot
+        L_b + t (L = cache_seqlens) and rotated at P_b + t, where
+        P = rotary_seqlens (default L);
+      * q row i of sequence b is rotated at P_b + i (causal or local) or P_b;
+      * the keys of sequence b are cache slots [lp_b, L_b + S_new(b)) with
+        lp = cache_leftpad (default 0): attention runs on the cache with its
+        first lp_b slots removed, so masks count keys from lp_b;
+      * attention_chunk c > 0 also restricts query i to the chunk of its
+        diagonal key.
+
+    Built from the pinned primitives kv_append, rotary and attention.
+    Returns (out, lse, k_cache_after, v_cache_after); lse is (B, H, Sq), or
+    (H, total_q) for ragged q."""
+    ragged_q = cu_seqlens_q is not None
+    cu_q = None if not ragged_q else np.asarray(cu_seqlens_q, dtype=np.int64)
+    B = len(cu_q) - 1 if ragged_q else q.shape[0]
+    H, D = q.shape[-2], q.shape[-1]
+    if softmax_scale is None:
+        softmax_scale = D ** -0.5
+    L = np.asarray(cache_seqlens, dtype=np.int64)
+    P = L if rotary_seqlens is None else np.asarray(rotary_seqlens, dtype=np.int64)
+    lp = np.zeros(B, np.int64) if cache_leftpad is None else np.asarray(cache_leftpad, dtype=np.int64)
+    crow = np.arange(B) if cache_batch_idx is None else np.asarray(cache_batch_idx, dtype=np.int64)
+    cu_n = None if cu_seqlens_k_new is None else np.asarray(cu_seqlens_k_new, dtype=np.int64)
+    kc = np.array(k_cache, dtype=np.uint16, copy=True, order="C")
+    vc = np.array(v_cache, dtype=np.uint16, copy=True, order="C")
+    out = np.zeros(q.shape, dtype=np.uint16)
+    if ragged_q:
+        lse = np.full((H, q.shape[0]), np.inf, dtype=np.float32)
+    else:
+        lse = np.full((B, H, q.shape[1]), np.inf, dtype=np.float32)
+    same = not (causal or window[0] >= 0 or window[1] >= 0)
+    for b in range(B):
+        s_new = 0
+        if k is not None:
+            if cu_n is not None:
+                kb, vb = k[cu_n[b]:cu_n[b + 1]][None], v[cu_n[b]:cu_n[b + 1]][None]
+            else:
+                kb, vb = k[b:b + 1], v[b:b + 1]
+            s_new = kb.shape[1]
+            if s_new > 0:
+                kc, vc = kv_append(kc, vc, kb, vb, L[b:b + 1], dtype=dtype, batch_idx=crow[b:b + 1],
+                                   block_table=block_table, cos=rotary_cos, sin=rotary_sin,
+                                   interleaved=rotary_interleaved, rot_pos=P[b:b + 1])
+        qb = q[cu_q[b]:cu_q[b + 1]][None] if ragged_q else q[b:b + 1]
+        if qb.shape[1] == 0:
+            continue
+        if k is not None and rotary_cos is not None:
+            qb = rotary(qb, rotary_cos, rotary_sin, P[b:b + 1], dtype=dtype, interleaved=rotary_interleaved,
+                        same_pos=same)
+        if block_table is None:
+            kv_k, kv_v = kc[crow[b]:crow[b] + 1, lp[b]:], vc[crow[b]:crow[b] + 1, lp[b]:]
+            bidx = None
+        else:
+            kv_k, kv_v, bidx = kc, vc, crow[b:b + 1]
+        ab = None
+        if alibi is not None:
+            al = np.asarray(alibi, dtype=np.float32)
+            ab = al[b] if al.ndim == 2 else al
+        ob, lb = attention(qb, kv_k, kv_v, dtype=dtype, scale=softmax_scale, softcap=softcap, causal=causal,
+                           window=window, alibi=ab, seqlens_k=np.array([L[b] + s_new - lp[b]]),
+                           block_table=block_table, batch_idx=bidx, nthreads=nthreads, chunk=attention_chunk)
+        if ragged_q:
+            out[cu_q[b]:cu_q[b + 1]] = ob[0]
+            lse[:, cu_q[b]:cu_q[b + 1]] = lb[0]
+        else:
+            out[b] = ob[0]
+            lse[b] = lb[0]
     return out, lse, kc, vc

@@ -27,8 +27,14 @@ def normalize_window(sq, sk, causal, wl, wr):
     return wl, wr, is_causal, is_local
 
 
-def mask_keep(sq, sk, causal=False, window=(-1, -1)):
-    """(sq, sk) bool, True = key visible (tests/fa_small_op_golden.py:35-58)."""
+def mask_keep(sq, sk, causal=False, window=(-1, -1), chunk=0):
+    """(sq, sk) bool, True = key visible (tests/fa_small_op_golden.py:35-58).
+    chunk > 0 (v3 attention_chunk) also keeps only keys whose chunk id
+    j // chunk equals that of the query's diagonal key i + sk - sq."""
+    if chunk > 0:
+        d = np.arange(sq)[:, None] + sk - sq
+        same = (np.arange(sk)[None, :] // chunk) == (d // chunk)
+        return mask_keep(sq, sk, causal, window) & same
     wl, wr, is_causal, is_local = normalize_window(sq, sk, causal, window[0], window[1])
     ones = np.ones((sq, sk))
     off = sk - sq
@@ -45,7 +51,7 @@ def mask_keep(sq, sk, causal=False, window=(-1, -1)):
     return masked == 0
 
 
-def attention(q, k, v, scale, causal=False, window=(-1, -1), alibi=None, softcap=0.0):
+def attention(q, k, v, scale, causal=False, window=(-1, -1), alibi=None, softcap=0.0, chunk=0):
     """One sequence. q (Sq, H, D), k (Sk, Hk, D), v (Sk, Hk, Dv), any float;
     alibi (H,) or None. Returns out (Sq, H, Dv) float64, lse (H, Sq) float64."""
     q = np.asarray(q, dtype=np.float64)
@@ -54,7 +60,7 @@ def attention(q, k, v, scale, causal=False, window=(-1, -1), alibi=None, softcap
     sq, h, _ = q.shape
     sk, hk, dv = v.shape
     g = h // hk
-    keep = mask_keep(sq, sk, causal, window)
+    keep = mask_keep(sq, sk, causal, window, chunk)
     out = np.zeros((sq, h, dv))
     lse = np.full((h, sq), np.inf)
     if sk == 0:
@@ -78,7 +84,7 @@ def attention(q, k, v, scale, causal=False, window=(-1, -1), alibi=None, softcap
     return out, lse
 
 
-def attention_batch(q, k, v, seqlens_k, scale, causal=False, window=(-1, -1), alibi=None, softcap=0.0):
+def attention_batch(q, k, v, seqlens_k, scale, causal=False, window=(-1, -1), alibi=None, softcap=0.0, chunk=0):
     """q (B, Sq, H, D); k, v (B, >=Sk_b, Hk, D); seqlens_k[b] keys of batch b.
     alibi (H,) or (B, H). Returns out (B, Sq, H, Dv), lse (B, H, Sq)."""
     B = q.shape[0]
@@ -88,7 +94,7 @@ def attention_batch(q, k, v, seqlens_k, scale, causal=False, window=(-1, -1), al
         if alibi is not None:
             al = alibi[b] if np.ndim(alibi) == 2 else alibi
         n = int(seqlens_k[b])
-        o, l = attention(q[b], k[b, :n], v[b, :n], scale, causal, window, al, softcap)
+        o, l = attention(q[b], k[b, :n], v[b, :n], scale, causal, window, al, softcap, chunk)
         outs.append(o)
         lses.append(l)
     return np.stack(outs), np.stack(lses)

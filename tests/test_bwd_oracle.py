@@ -10,9 +10,10 @@ import pytest
 import torch
 
 from oracle import fa_bwd_oracle as bo
+from tests.golden import brute
 
 
-def _fwd_autograd(q, k, v, dout, *, scale, softcap, causal, window, alibi):
+def _fwd_autograd(q, k, v, dout, *, scale, softcap, causal, window, alibi, chunk=0):
     """q (H, Sq, D), k/v (Hk, Sk, D) float64 tensors with grad; one sequence."""
     H, sq, _ = q.shape
     Hk, sk, _ = k.shape
@@ -26,7 +27,8 @@ def _fwd_autograd(q, k, v, dout, *, scale, softcap, causal, window, alibi):
         i = torch.arange(sq, dtype=torch.float64)[:, None]
         j = torch.arange(sk, dtype=torch.float64)[None, :]
         s = s - alibi[:, None, None] * (i + sk - sq - j).abs()[None]
-    keep = torch.from_numpy(bo._visible(sq, sk, causal, *window))
+    # the mask from the brute force's triangular-matrix / chunk-id construction
+    keep = torch.from_numpy(brute.mask_keep(sq, sk, causal, window, chunk))
     s = s.masked_fill(~keep[None], float("-inf"))
     lse = torch.logsumexp(s, dim=-1)
     out = torch.softmax(s, dim=-1) @ vb
@@ -43,12 +45,16 @@ CASES = [
     (6, 3, 20, 28, 16, False, (-1, -1), 2.0, False),      # strong soft cap
     (4, 4, 19, 19, 16, True, (-1, -1), 0.0, True),        # ALiBi
     (8, 4, 12, 50, 24, False, (10, 10), 5.0, True),       # everything
+    (4, 2, 40, 40, 16, True, (-1, -1), 0.0, False, 8),    # attention_chunk
+    (4, 4, 23, 37, 16, False, (-1, -1), 0.0, False, 10),  # chunk, non-causal, Sk > Sq
+    (4, 2, 18, 30, 8, True, (6, 0), 3.0, True, 5),        # chunk with window, soft cap, ALiBi
 ]
 
 
 @pytest.mark.parametrize("case", CASES, ids=[str(i) for i in range(len(CASES))])
 def test_oracle_bwd_matches_autograd(case):
-    H, Hk, sq, sk, D, causal, window, softcap, use_alibi = case
+    H, Hk, sq, sk, D, causal, window, softcap, use_alibi = case[:9]
+    chunk = case[9] if len(case) > 9 else 0
     g = torch.Generator().manual_seed(sum(case[:5]))
     q = torch.randn(H, sq, D, generator=g, dtype=torch.float64, requires_grad=True)
     k = torch.randn(Hk, sk, D, generator=g, dtype=torch.float64, requires_grad=True)
@@ -57,12 +63,12 @@ def test_oracle_bwd_matches_autograd(case):
     alibi = torch.rand(H, generator=g, dtype=torch.float64) * 0.5 if use_alibi else None
     scale = D ** -0.5
     lse, out, dq, dk, dv = _fwd_autograd(q, k, v, dout, scale=scale, softcap=softcap, causal=causal, window=window,
-                                         alibi=alibi)
+                                         alibi=alibi, chunk=chunk)
     # dense layout: (B=1, S, H, D)
     to_bshd = lambda t: t.detach().numpy().transpose(1, 0, 2)[None]
     rq, rk, rv = bo.attention_bwd(to_bshd(q), to_bshd(k), to_bshd(v), to_bshd(dout), lse.numpy()[None],
                                   scale=scale, softcap=softcap, causal=causal, window=window,
-                                  alibi=None if alibi is None else alibi.numpy())
+                                  alibi=None if alibi is None else alibi.numpy(), chunk=chunk)
     for got, ref in ((rq, dq), (rk, dk), (rv, dv)):
         np.testing.assert_allclose(got[0].transpose(1, 0, 2), ref.numpy(), rtol=1e-9, atol=1e-10)
     # the dsum helper is rowsum(dout * out)

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(capi):
     for n in names:
         assert hasattr(lib, n), f"libfa_mi355x.so does not export {n}"
     assert sorted(capi.EXPORTED) == names
-    assert capi.lib().fa_abi_version() == capi.ABI_VERSION == 1
+    assert capi.lib().fa_abi_version() == capi.ABI_VERSION == 2
 
 
 @pytest.mark.parametrize("struct", ["fa_fwd_params", "fa_bwd_params"])
@@ -88,6 +88,7 @@ def test_validate_bwd(capi):
         (dict(softcap=-1.0), capi.FA_KIND_DENSE, capi.FA_EINVAL, "softcap"),
         (dict(dq=0x10008), capi.FA_KIND_DENSE, capi.FA_EINVAL, "16-byte aligned"),
         (dict(softmax_d=None), capi.FA_KIND_DENSE, capi.FA_EINVAL, "softmax_d"),
+        (dict(attention_chunk=-1), capi.FA_KIND_DENSE, capi.FA_EINVAL, "attention_chunk"),
         (dict(), capi.FA_KIND_VARLEN, capi.FA_EINVAL, "cu_seqlens_q and cu_seqlens_k are required"),
         (dict(), capi.FA_KIND_KVCACHE, capi.FA_EINVAL, "dense or varlen"),
     ]
@@ -116,6 +117,12 @@ def test_validate_accepts_a_valid_call(capi):
     assert capi.validate(_valid(capi, k_new=0x70000, v_new=0x80000, seqlen_new=1, knew_batch_stride=256,
                                 knew_row_stride=256, knew_head_stride=128, vnew_batch_stride=256,
                                 vnew_row_stride=256, vnew_head_stride=128), capi.FA_KIND_KVCACHE) == capi.FA_OK
+    # v3 kvcache extensions: ragged q and new tokens, leftpad, rotary positions, chunked attention
+    assert capi.validate(_valid(capi, k_new=0x70000, v_new=0x80000, cu_seqlens_k_new=0xE0000, total_k_new=5,
+                                knew_row_stride=256, knew_head_stride=128, vnew_row_stride=256,
+                                vnew_head_stride=128, cu_seqlens_q=0xF0000, total_q=7, cache_leftpad=0xD0000,
+                                attention_chunk=64), capi.FA_KIND_KVCACHE) == capi.FA_OK
+    assert capi.validate(_valid(capi, attention_chunk=128), capi.FA_KIND_DENSE) == capi.FA_OK
 
 
 BAD = [
@@ -140,6 +147,12 @@ BAD = [
     (dict(alibi_slopes=ctypes.cast(0xC0000, ctypes.c_void_p), alibi_batch_stride=3), 0, "EINVAL", "alibi_slopes"),
     (dict(), 2, "EINVAL", "cu_seqlens_q is required"),
     (dict(block_table=0xB0000, page_block_size=16, max_blocks_per_seq=1), 1, "EINVAL", "dense forward"),
+    (dict(attention_chunk=-4), 1, "EINVAL", "attention_chunk"),
+    (dict(cache_leftpad=0xD0000, block_table=0xB0000, page_block_size=16, max_blocks_per_seq=1,
+          block_table_rows=2), 0, "EINVAL", "cache_leftpad is not supported with a paged"),
+    (dict(cu_seqlens_k_new=0xE0000, total_k_new=3), 0, "EINVAL", "without new keys"),
+    (dict(cache_leftpad=0xD0000), 1, "EINVAL", "only valid for the kvcache forward"),
+    (dict(cu_seqlens_q=0xF0000, total_q=-1), 0, "EINVAL", "total_q must be >= 0"),
 ]
 
 

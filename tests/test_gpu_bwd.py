@@ -31,11 +31,12 @@ def check(name, got, ref):
     assert not bad.any(), f"{name}: {int(bad.sum())} elements out of tolerance, max err {err.max():.3e}"
 
 
-def run_dense(dtype, B, H, Hk, Sq, Sk, D, causal, window=(-1, -1), softcap=0.0, alibi=False, api="v2", seed=0):
+def run_dense(dtype, B, H, Hk, Sq, Sk, D, causal, window=(-1, -1), softcap=0.0, alibi=False, api="v2", seed=0,
+              chunk=0):
     import flash_attn_npu_v2
     import flash_attn_npu_v3
     print(f"case bwd dense {api} {dtype} B{B} H{H}/{Hk} {Sq}x{Sk} D{D} causal={causal} window={window} "
-          f"softcap={softcap} alibi={alibi}", flush=True)
+          f"softcap={softcap} alibi={alibi} chunk={chunk}", flush=True)
     g = torch.Generator().manual_seed(seed)
     q = rand_inputs((B, Sq, H, D), dtype, g)
     k = rand_inputs((B, Sk, Hk, D), dtype, g)
@@ -50,18 +51,18 @@ def run_dense(dtype, B, H, Hk, Sq, Sk, D, causal, window=(-1, -1), softcap=0.0, 
                                                         return_attn_probs=True)
     else:
         out, lse = flash_attn_npu_v3.flash_attn_func(qd, kd, vd, causal=causal, window_size=window, softcap=softcap,
-                                                     return_attn_probs=True)
+                                                     attention_chunk=chunk, return_attn_probs=True)
     dq, dk, dv = torch.autograd.grad(out, (qd, kd, vd), do.to(DEV))
     torch.cuda.synchronize()
     rq, rk, rv = bo.attention_bwd(q.float().numpy(), k.float().numpy(), v.float().numpy(), do.float().numpy(),
                                   lse.detach().cpu().numpy(), scale=scale, softcap=softcap, causal=causal,
-                                  window=window, alibi=None if slopes is None else slopes.numpy())
+                                  window=window, alibi=None if slopes is None else slopes.numpy(), chunk=chunk)
     check("dq", dq, rq)
     check("dk", dk, rk)
     check("dv", dv, rv)
 
 
-def run_varlen(dtype, H, Hk, lq, lk, D, causal, window=(-1, -1), softcap=0.0, api="v2", seed=0):
+def run_varlen(dtype, H, Hk, lq, lk, D, causal, window=(-1, -1), softcap=0.0, api="v2", seed=0, chunk=0):
     import flash_attn_npu_v2
     import flash_attn_npu_v3
     print(f"case bwd varlen {api} {dtype} H{H}/{Hk} lq={lq} lk={lk} D{D} causal={causal} window={window} "
@@ -77,14 +78,15 @@ def run_varlen(dtype, H, Hk, lq, lk, D, causal, window=(-1, -1), softcap=0.0, ap
     qd, kd, vd = (x.to(DEV).requires_grad_(True) for x in (q, k, v))
     cqd, ckd = torch.from_numpy(cq).to(DEV), torch.from_numpy(ck).to(DEV)
     f = flash_attn_npu_v2.flash_attn_varlen_func if api == "v2" else flash_attn_npu_v3.flash_attn_varlen_func
+    kw = dict(attention_chunk=chunk) if chunk else {}
     res = f(qd, kd, vd, cqd, ckd, max(lq), max(lk), causal=causal, window_size=window, softcap=softcap,
-            return_attn_probs=True)
+            return_attn_probs=True, **kw)
     out, lse = res[0], res[1]
     dq, dk, dv = torch.autograd.grad(out, (qd, kd, vd), do.to(DEV))
     torch.cuda.synchronize()
     rq, rk, rv = bo.attention_bwd(q.float().numpy(), k.float().numpy(), v.float().numpy(), do.float().numpy(),
                                   lse.detach().cpu().numpy(), scale=scale, softcap=softcap, causal=causal,
-                                  window=window, cu_seqlens_q=cq, cu_seqlens_k=ck)
+                                  window=window, cu_seqlens_q=cq, cu_seqlens_k=ck, chunk=chunk)
     check("dq", dq, rq)
     check("dk", dk, rk)
     check("dv", dv, rv)
@@ -226,3 +228,19 @@ def test_bwd_softmax_d_returned():
     torch.cuda.synchronize()
     ref = bo.softmax_d(out.float().cpu().numpy(), do.float().cpu().numpy())
     np.testing.assert_allclose(sd.cpu().numpy(), ref, rtol=1e-4, atol=1e-4)
+
+
+# attention_chunk (v3 API): the chunk cuts the causal / local band
+@pytest.mark.parametrize("case", [
+    (torch.bfloat16, 2, 4, 2, 512, 512, 128, True, (-1, -1), 64),
+    (torch.float16, 1, 4, 4, 300, 700, 128, False, (-1, -1), 100),
+    (torch.bfloat16, 2, 4, 1, 384, 384, 64, True, (90, 0), 128),
+    (torch.bfloat16, 1, 4, 2, 200, 456, 256, True, (-1, -1), 48),
+], ids=["causal64", "noncausal100", "window_d64", "d256"])
+def test_bwd_chunk(case):
+    dtype, B, H, Hk, Sq, Sk, D, causal, window, chunk = case
+    run_dense(dtype, B, H, Hk, Sq, Sk, D, causal, window=window, api="v3", seed=B + H + Sq, chunk=chunk)
+
+
+def test_bwd_varlen_chunk():
+    run_varlen(torch.bfloat16, 4, 2, [130, 1, 260, 77], [130, 40, 300, 77], 128, True, api="v3", seed=9, chunk=96)
