@@ -90,7 +90,7 @@ struct Plan {
     int grid;
     bool rotary;
     int workers;        // decode: wave workers
-    int kd;             // kernel head dim (128 or 256)
+    int kd;             // kernel head dim (64, 128 or 256)
     size_t off_sched, off_plse, off_po, off_qrot, total;
 };
 
@@ -191,11 +191,12 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
 void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
     pl.g = p->nheads / p->nheads_k;
     pl.rows_max = p->seqlen_q * pl.g;
-    // kernel head dim: the 128 kernels serve head dims up to 128 (the dims
-    // above the real ones read as zero), the 256 prefill kernel the rest;
-    // decode shapes above 128 run on the prefill kernel
-    pl.kd = p->headdim <= 128 ? 128 : 256;
-    pl.decode = pl.rows_max <= kDecodeRows && pl.kd == 128;
+    // kernel head dim: the prefill kernels come at 64, 128 and 256 and serve
+    // the head dims up to theirs (the dims above the real ones read as zero);
+    // the decode kernel serves head dims up to 128, decode shapes above 128
+    // run on the prefill kernel
+    pl.decode = pl.rows_max <= kDecodeRows && p->headdim <= 128;
+    pl.kd = pl.decode ? 128 : p->headdim <= 64 ? 64 : p->headdim <= 128 ? 128 : 256;
     pl.BM = pl.decode ? kDecodeRows : fa::fwd_tile_rows(pl.kd);
     pl.BN = pl.decode ? 32 : fa::fwd_tile_keys(pl.kd);
     pl.mt_max = (pl.rows_max + pl.BM - 1) / pl.BM;

@@ -67,6 +67,12 @@ __device__ __forceinline__ float f16_to_32(uint16_t h) {
 // the ds_read_b64_tr_b16 transpose reads of 4-row groups.
 __device__ __forceinline__ int swz_k(int r, int c) { return c ^ (r & 15); }
 __device__ __forceinline__ int swz_v(int r, int c) { return c ^ ((r & 3) << 1) ^ (((r >> 2) & 1) << 3); }
+// The same for 128-byte rows (head dim 64, 8 chunks): row r starts at bank
+// 32 * (r & 1), so the XOR comes from the row bits above the parity. K: the 16
+// rows of a 16-byte operand read hit 16 different 4-bank groups. V: the 8 rows
+// a half wave of transpose reads covers take 4 disjoint chunk pairs per parity.
+__device__ __forceinline__ int swz_k64(int r, int c) { return c ^ ((r >> 1) & 7); }
+__device__ __forceinline__ int swz_v64(int r, int c) { return c ^ (((r >> 1) & 3) << 1); }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }

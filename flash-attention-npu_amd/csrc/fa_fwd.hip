@@ -191,7 +191,7 @@ constexpr float kLazy = 8.f;       // log2 headroom before the running max moves
 template <int HD>
 struct PfCfg {
     static constexpr int D = HD;
-    static constexpr int RB = HD > 128 ? 1 : PF_RB;   // 16-row blocks per wave
+    static constexpr int RB = HD > 128 ? 1 : HD == 64 ? 4 : PF_RB;  // 16-row blocks per wave
     static constexpr int NW = PF_NW;                  // waves per workgroup
     static constexpr int NT = NW * 64;
     static constexpr int BM = NW * RB * 16;           // packed rows per work tile
@@ -224,18 +224,21 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
     int total, chunk_auto;
     build_schedule<BM, BN, NT, NW>(a, s_pref, s_red, total, chunk_auto);
 
+    // LDS swizzles for the row length (128-byte rows at head dim 64)
+    auto swzk = [](int r, int c) { return HD == 64 ? swz_k64(r, c) : swz_k(r, c); };
+    auto swzv = [](int r, int c) { return HD == 64 ? swz_v64(r, c) : swz_v(r, c); };
     // loop-invariant LDS offsets (elements)
     int offk[KSTEPS];
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) offk[s] = li * D + (swz_k(li, G * KSTEPS + s) << 3);
+    for (int s = 0; s < KSTEPS; ++s) offk[s] = li * D + (swzk(li, G * KSTEPS + s) << 3);
     const int r4 = li >> 2, c4 = li & 3;
     int offv[DBLK];
 #pragma unroll
     for (int db = 0; db < DBLK; ++db)
-        offv[db] = (4 * G + r4) * D + (swz_v(4 * G + r4, 2 * db + (c4 >> 1)) << 3) + (c4 & 1) * 4;
+        offv[db] = (4 * G + r4) * D + (swzv(4 * G + r4, 2 * db + (c4 >> 1)) << 3) + (c4 & 1) * 4;
     const int dch = tid & (DCH - 1), kk0 = tid / DCH;
-    const int offsk = kk0 * D + (swz_k(kk0, dch) << 3);   // + u*(NT/DCH)*D for chunk u
-    const int offsv = kk0 * D + (swz_v(kk0, dch) << 3);
+    const int offsk = kk0 * D + (swzk(kk0, dch) << 3);   // + u*(NT/DCH)*D for chunk u
+    const int offsv = kk0 * D + (swzv(kk0, dch) << 3);
 
     const uint16_t* qp = static_cast<const uint16_t*>(a.q);
     const uint16_t* kp = static_cast<const uint16_t*>(a.k);
@@ -711,8 +714,8 @@ __global__ void __launch_bounds__(256) fa_combine_flat_kernel(const float* __res
 }
 
 // ---- host-side launchers (called from fa_api.cpp) -------------------------------------
-int fwd_tile_rows(int d) { return d > 128 ? PfCfg<256>::BM : PfCfg<128>::BM; }
-int fwd_tile_keys(int d) { return d > 128 ? PfCfg<256>::BN : PfCfg<128>::BN; }
+int fwd_tile_rows(int d) { return d > 128 ? PfCfg<256>::BM : d > 64 ? PfCfg<128>::BM : PfCfg<64>::BM; }
+int fwd_tile_keys(int d) { return d > 128 ? PfCfg<256>::BN : d > 64 ? PfCfg<128>::BN : PfCfg<64>::BN; }
 
 template <int DT, int HD, bool BIAS, bool ROT>
 static void launch_prefill_r(const FwdArgs& a, int grid, hipStream_t stream) {
@@ -739,9 +742,10 @@ static void launch_prefill_d(const FwdArgs& a, int dtype, int grid, hipStream_t 
     }
 }
 
-// d: the kernel head dim, 128 or 256 (a.hd <= d is the head dim in memory)
+// d: the kernel head dim, 64, 128 or 256 (a.hd <= d is the head dim in memory)
 hipError_t launch_fwd(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream) {
-    if (d == 128) launch_prefill_d<128>(a, dtype, grid, stream);
+    if (d == 64) launch_prefill_d<64>(a, dtype, grid, stream);
+    else if (d == 128) launch_prefill_d<128>(a, dtype, grid, stream);
     else if (d == 256) launch_prefill_d<256>(a, dtype, grid, stream);
     else return hipErrorInvalidValue;
     return hipGetLastError();
@@ -757,7 +761,8 @@ static void launch_merge_d(const FwdArgs& a, int dtype, hipStream_t stream) {
 }
 
 hipError_t launch_merge(const FwdArgs& a, int dtype, int d, hipStream_t stream) {
-    if (d == 128) launch_merge_d<128>(a, dtype, stream);
+    if (d == 64) launch_merge_d<64>(a, dtype, stream);
+    else if (d == 128) launch_merge_d<128>(a, dtype, stream);
     else if (d == 256) launch_merge_d<256>(a, dtype, stream);
     else return hipErrorInvalidValue;
     return hipGetLastError();

@@ -213,6 +213,29 @@ def test_headdim_chunked_prefill_rotary(rotary):
     run_kvcache(2, 80, 16, 4, 64, torch.bfloat16, 400, [200, 57], s_new=80, rotary=rotary, causal=True, seed=53)
 
 
+# ---- head dims up to 64: the 64 prefill kernel (64 rows per wave, 128-byte LDS rows) ---------
+@pytest.mark.parametrize("D", [32, 48, 64])
+def test_headdim64_dense_noncausal(D):
+    print(f"case headdim64 dense non-causal D={D}", flush=True)
+    run_dense(2, 300, 170, 8, 4, D, torch.bfloat16, causal=False, seed=70 + D)
+
+
+def test_headdim64_window_softcap_alibi():
+    print("case headdim64 window softcap alibi", flush=True)
+    run_dense(2, 257, 600, 8, 2, 64, torch.float16, causal=True, window=(100, 0), softcap=20.0, alibi=True, seed=74)
+
+
+def test_headdim64_split_few_rows():
+    print("case headdim64 split over the keys", flush=True)
+    run_dense(1, 40, 5000, 4, 1, 64, torch.bfloat16, causal=True, seed=75)
+
+
+def test_headdim64_paged_chunked_prefill_rotary():
+    print("case headdim64 paged chunked prefill rotary", flush=True)
+    run_kvcache(3, 70, 16, 4, 64, torch.bfloat16, 0, [300, 0, 129], s_new=70, page=32, rotary="neox", causal=True,
+                seed=76)
+
+
 # ---- head dims above 128: the 256 prefill kernel (decode shapes run on it too) --------------
 @pytest.mark.parametrize("D", [136, 192, 256])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
