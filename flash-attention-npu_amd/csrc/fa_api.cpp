@@ -27,8 +27,8 @@ int fwd_tile_keys(int d);
 int decode_workers(int cus);
 hipError_t launch_fwd(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream);
 hipError_t launch_merge(const FwdArgs& a, int dtype, int d, hipStream_t stream);
-hipError_t launch_decode(const FwdArgs& a, int dtype, int grid, hipStream_t stream);
-hipError_t launch_decode_merge(const FwdArgs& a, int dtype, int grid, hipStream_t stream);
+hipError_t launch_decode(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream);
+hipError_t launch_decode_merge(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream);
 hipError_t launch_combine_flat(const float* po, const float* pl, int S, int64_t R, int Dv, void* out, int64_t ors,
                                int out_dtype, float* lse, hipStream_t stream);
 hipError_t launch_kv_prep(const KvPrepArgs& a, int dtype, hipStream_t stream);
@@ -191,12 +191,12 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
 void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
     pl.g = p->nheads / p->nheads_k;
     pl.rows_max = p->seqlen_q * pl.g;
-    // kernel head dim: the prefill kernels come at 64, 128 and 256 and serve
-    // the head dims up to theirs (the dims above the real ones read as zero);
-    // the decode kernel serves head dims up to 128, decode shapes above 128
+    // kernel head dim: the prefill kernels come at 64, 128 and 256, the
+    // decode kernel at 64 and 128; each serves the head dims up to its own
+    // (the dims above the real ones read as zero); decode shapes above 128
     // run on the prefill kernel
     pl.decode = pl.rows_max <= kDecodeRows && p->headdim <= 128;
-    pl.kd = pl.decode ? 128 : p->headdim <= 64 ? 64 : p->headdim <= 128 ? 128 : 256;
+    pl.kd = p->headdim <= 64 ? 64 : p->headdim <= 128 ? 128 : 256;
     pl.BM = pl.decode ? kDecodeRows : fa::fwd_tile_rows(pl.kd);
     pl.BN = pl.decode ? 32 : fa::fwd_tile_keys(pl.kd);
     pl.mt_max = (pl.rows_max + pl.BM - 1) / pl.BM;
@@ -438,12 +438,12 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
     }
 
     mark(1);
-    hipError_t e = pl.decode ? fa::launch_decode(a, p->dtype, pl.grid, stream)
+    hipError_t e = pl.decode ? fa::launch_decode(a, p->dtype, pl.kd, pl.grid, stream)
                              : fa::launch_fwd(a, p->dtype, pl.kd, pl.grid, stream);
     if (e != hipSuccess) return fail(FA_EHIP, "attention launch failed: %s", hipGetErrorString(e));
     mark(2);
     if (pl.decode) {
-        hipError_t em = fa::launch_decode_merge(a, p->dtype, pl.grid, stream);
+        hipError_t em = fa::launch_decode_merge(a, p->dtype, pl.kd, pl.grid, stream);
         if (em != hipSuccess) return fail(FA_EHIP, "merge launch failed: %s", hipGetErrorString(em));
     } else if (pl.allow_split) {
         hipError_t em = fa::launch_merge(a, p->dtype, pl.kd, stream);

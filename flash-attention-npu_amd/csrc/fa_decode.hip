@@ -24,15 +24,24 @@
 
 namespace fa {
 namespace dec {
-constexpr int D = 128;
-constexpr int KT = 32;       // keys per tile
 constexpr int NWAVE = 4;     // waves (workers) per workgroup
-constexpr int KSTEPS = D / 32;
-constexpr int DBLK = D / 16;
-constexpr int SWZ = 15;
 constexpr int TABN = 256;    // paged: block ids staged per wave
 constexpr int MAXB = 2048;
 }  // namespace dec
+
+// Tile shape per kernel head dim: a tile is 16 KB of K and V (32 keys at head
+// dim 128, 64 keys at 64), so a wave keeps the same bytes in flight and every
+// lane loads full 16-byte chunks at both head dims.
+template <int HD>
+struct DecCfg {
+    static constexpr int D = HD;
+    static constexpr int KT = 4096 / HD;   // keys per tile
+    static constexpr int NH = KT / 16;     // 16-key blocks per tile
+    static constexpr int KSTEPS = D / 32;
+    static constexpr int DBLK = D / 16;
+    // 16-byte chunk swizzle of the wave's V tile (row-major, D / 8 chunks per row)
+    static __device__ __forceinline__ int vswz(int r, int c) { return HD == 64 ? swz_v64(r, c) : (c ^ (r & 15)); }
+};
 
 struct DecSeg {
     int S, n;         // first global tile, tiles
@@ -47,6 +56,7 @@ struct DecBatch {
     int lo_tile, sk, sq, crow, lp;
 };
 
+template <int KT>
 __device__ __forceinline__ void dec_batch(const FwdArgs& a, int b, DecBatch& d, int& ntiles) {
     int sq = a.cu_seqlens_q ? a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b] : a.Sq;
     int sk;
@@ -61,10 +71,10 @@ __device__ __forceinline__ void dec_batch(const FwdArgs& a, int b, DecBatch& d, 
     d.lp = lp;
     d.sq = sq;
     d.sk = sk;
-    d.lo_tile = lo / dec::KT;
+    d.lo_tile = lo / KT;
     const int bt_rows_or_cache = a.block_table ? a.bt_rows : a.batch_cache;
     d.crow = a.batch_idx ? min(max(a.batch_idx[b], 0), bt_rows_or_cache - 1) : b;
-    ntiles = (sq > 0 && hi > lo) ? (hi + dec::KT - 1) / dec::KT - d.lo_tile : 0;
+    ntiles = (sq > 0 && hi > lo) ? (hi + KT - 1) / KT - d.lo_tile : 0;
 }
 
 __device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref, const DecBatch* s_b, int t) {
@@ -92,9 +102,11 @@ __device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref
 // BIAS: softcap or ALiBi present; FUSE: append k_new/v_new in this kernel;
 // LAYOUT: 0 = batch-strided cache, 1 = paged with page % 32 == 0, 2 = any;
 // HDM: head dim below 128 (dims >= a.hd read as zero, never written).
-template <int DT, int STAGES, bool BIAS, bool FUSE, int LAYOUT, bool HDM = false>
+template <int DT, int HD, int STAGES, bool BIAS, bool FUSE, int LAYOUT, bool HDM = false>
 __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     using namespace dec;
+    using C = DecCfg<HD>;
+    constexpr int D = C::D, KT = C::KT, NH = C::NH, KSTEPS = C::KSTEPS, DBLK = C::DBLK;
     __shared__ int s_pref[MAXB + 1];
     __shared__ DecBatch s_bat[MAXB];
     __shared__ int s_tab[NWAVE][TABN];
@@ -107,7 +119,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     for (int b = tid; b < a.B; b += 256) {
         DecBatch d;
         int nt;
-        dec_batch(a, b, d, nt);
+        dec_batch<KT>(a, b, d, nt);
         s_bat[b] = d;
         s_pref[b + 1] = a.Hk * nt;
     }
@@ -167,7 +179,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     if (tab_ok) fill_tab(tab_base);
 
     // ---- issue side: STAGES-deep register pipeline ------------------------------------
-    u32x4 kr[STAGES][2][KSTEPS], vr[STAGES][2][KSTEPS];
+    u32x4 kr[STAGES][NH][KSTEPS], vr[STAGES][NH][KSTEPS];
     int bk[STAGES];  // paged block id of each in-flight tile
     DecSeg is = dec_seg_of(a, s_pref, s_bat, t0);
 
@@ -193,7 +205,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     const uint16_t* knp = static_cast<const uint16_t*>(a.k_new);
     const uint16_t* vnp = static_cast<const uint16_t*>(a.v_new);
 
-    auto issue = [&](int t, u32x4 (&kk)[2][KSTEPS], u32x4 (&vv)[2][KSTEPS], int& blk) {
+    auto issue = [&](int t, u32x4 (&kk)[NH][KSTEPS], u32x4 (&vv)[NH][KSTEPS], int& blk) {
         if (t >= t1) return;
         if (t >= is.S + is.n) is = dec_seg_of(a, s_pref, s_bat, t);
         blk = 0;
@@ -207,22 +219,22 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         const int key0 = (is.lo_tile + (t - is.S)) * KT;
         const int first_new = fuse ? is.sk - a.seqlen_new : 0x7fffffff;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < NH; ++h) {
             const int key = key0 + h * 16 + li;
             if (key < is.sk) {
                 const uint16_t* kpr;
                 const uint16_t* vpr;
                 if (key >= first_new) {
                     const int tn = key - first_new;
-                    kpr = knp + (int64_t)is.b * a.kn_sb + (int64_t)tn * a.kn_si + (int64_t)is.hk * a.kn_sh + G * 32;
-                    vpr = vnp + (int64_t)is.b * a.vn_sb + (int64_t)tn * a.vn_si + (int64_t)is.hk * a.vn_sh + G * 32;
+                    kpr = knp + (int64_t)is.b * a.kn_sb + (int64_t)tn * a.kn_si + (int64_t)is.hk * a.kn_sh + G * (D / 4);
+                    vpr = vnp + (int64_t)is.b * a.vn_sb + (int64_t)tn * a.vn_si + (int64_t)is.hk * a.vn_sh + G * (D / 4);
                 } else {
-                    kpr = row_ptr(kp, a.k_sb, a.k_si, a.k_sh, is, key, blk) + G * 32;
-                    vpr = row_ptr(vp, a.v_sb, a.v_si, a.v_sh, is, key, blk) + G * 32;
+                    kpr = row_ptr(kp, a.k_sb, a.k_si, a.k_sh, is, key, blk) + G * (D / 4);
+                    vpr = row_ptr(vp, a.v_sb, a.v_si, a.v_sh, is, key, blk) + G * (D / 4);
                 }
 #pragma unroll
                 for (int s = 0; s < KSTEPS; ++s) {
-                    const bool in = !HDM || G * 32 + s * 8 < a.hd;
+                    const bool in = !HDM || G * (D / 4) + s * 8 < a.hd;
                     kk[h][s] = in ? *reinterpret_cast<const u32x4*>(kpr + s * 8) : u32x4{0u, 0u, 0u, 0u};
                     vv[h][s] = in ? *reinterpret_cast<const u32x4*>(vpr + s * 8) : u32x4{0u, 0u, 0u, 0u};
                 }
@@ -302,7 +314,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         }
     };
 
-    auto compute = [&](int t, const u32x4 (&kk)[2][KSTEPS], const u32x4 (&vv)[2][KSTEPS], int blk) {
+    auto compute = [&](int t, const u32x4 (&kk)[NH][KSTEPS], const u32x4 (&vv)[NH][KSTEPS], int blk) {
         const int key0 = (cs.lo_tile + (t - cs.S)) * KT;
         if (fuse && key0 + KT > cs.sk - a.seqlen_new) {
             // this tile holds appended tokens: write them into the cache
@@ -310,14 +322,14 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             uint16_t* kc = const_cast<uint16_t*>(kp);
             uint16_t* vc = const_cast<uint16_t*>(vp);
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
+            for (int h = 0; h < NH; ++h) {
                 const int key = key0 + h * 16 + li;
                 if (key >= first_new && key < cs.sk) {
-                    uint16_t* kd = const_cast<uint16_t*>(row_ptr(kc, a.k_sb, a.k_si, a.k_sh, cs, key, blk)) + G * 32;
-                    uint16_t* vd = const_cast<uint16_t*>(row_ptr(vc, a.v_sb, a.v_si, a.v_sh, cs, key, blk)) + G * 32;
+                    uint16_t* kd = const_cast<uint16_t*>(row_ptr(kc, a.k_sb, a.k_si, a.k_sh, cs, key, blk)) + G * (D / 4);
+                    uint16_t* vd = const_cast<uint16_t*>(row_ptr(vc, a.v_sb, a.v_si, a.v_sh, cs, key, blk)) + G * (D / 4);
 #pragma unroll
                     for (int s = 0; s < KSTEPS; ++s) {
-                        if (!HDM || G * 32 + s * 8 < a.hd) {
+                        if (!HDM || G * (D / 4) + s * 8 < a.hd) {
                             *reinterpret_cast<u32x4*>(kd + s * 8) = kk[h][s];
                             *reinterpret_cast<u32x4*>(vd + s * 8) = vv[h][s];
                         }
@@ -327,28 +339,29 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         }
         // V tile -> wave-private LDS (row-major, 16-byte XOR swizzle)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < NH; ++h) {
             const int kl = h * 16 + li;
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s) {
                 const int ch = G * KSTEPS + s;
-                *reinterpret_cast<u32x4*>(sv + kl * D + ((ch ^ (kl & SWZ)) << 3)) = vv[h][s];
+                *reinterpret_cast<u32x4*>(sv + kl * D + (C::vswz(kl, ch) << 3)) = vv[h][s];
             }
         }
         // S^T = K . Q^T
-        f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        f32x4 sacc[NH];
 #pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) {
-            sacc[0] = mfma16x16x32<DT>(kk[0][s], qreg[s], sacc[0]);
-            sacc[1] = mfma16x16x32<DT>(kk[1][s], qreg[s], sacc[1]);
-        }
+        for (int h = 0; h < NH; ++h) sacc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+            for (int h = 0; h < NH; ++h) sacc[h] = mfma16x16x32<DT>(kk[h][s], qreg[s], sacc[h]);
         // online softmax (log2 domain), row = li, keys key0 + 16h + 4G + e
         const int sk = cs.sk, diag0 = cs.sk - cs.sq;
         const bool full = key0 + KT <= sk && key0 >= seg_flo && key0 + KT - 1 <= seg_fhi;
         constexpr bool plain = !BIAS;
-        float x[2][4];
+        float x[NH][4];
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < NH; ++h)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float sv2 = sacc[h][e];
@@ -371,7 +384,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             const int dg = qi + diag0;
             const int rlo = key_lo(dg, a.wl, a.chunk), rhi = key_hi(dg, a.wr, a.chunk);
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
+            for (int h = 0; h < NH; ++h)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int j = key0 + h * 16 + G * 4 + e;
@@ -379,37 +392,49 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                     x[h][e] = vis ? x[h][e] : -INFINITY;
                 }
         }
-        float tmax = fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
-                           fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) tmax = fmaxf(tmax, fmaxf(fmaxf(x[h][0], x[h][1]), fmaxf(x[h][2], x[h][3])));
         tmax = wave_max16x4(tmax);
         const float m_new = fmaxf(m_run, tmax);
         const float m_use = m_new == -INFINITY ? 0.f : m_new;
         const float alpha = fast_exp2(m_run - m_use);
         m_run = m_new;
-        float p[2][4], psum = 0.f;
+        float p[NH][4], psum = 0.f;
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < NH; ++h)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 p[h][e] = fast_exp2(x[h][e] - m_use);
                 psum += p[h][e];
             }
         l_run = l_run * alpha + psum;
-        f32x8 p8 = {p[0][0], p[0][1], p[0][2], p[0][3], p[1][0], p[1][1], p[1][2], p[1][3]};
-        const u32x4 pk = pack8<DT>(p8);
+        // P^T operands, one per 32 keys: blocks 2k and 2k + 1
+        u32x4 pk[NH / 2];
+#pragma unroll
+        for (int k2 = 0; k2 < NH / 2; ++k2) {
+            f32x8 p8 = {p[2 * k2][0], p[2 * k2][1], p[2 * k2][2], p[2 * k2][3],
+                        p[2 * k2 + 1][0], p[2 * k2 + 1][1], p[2 * k2 + 1][2], p[2 * k2 + 1][3]};
+            pk[k2] = pack8<DT>(p8);
+        }
         // O^T += V^T . P^T with V^T from transpose reads of the LDS tile
         const int r4 = li >> 2, c4 = li & 3;
-        const int ka = 4 * G + r4, kb = ka + 16;
 #pragma unroll
         for (int db = 0; db < DBLK; ++db) {
             const int ch = 2 * db + (c4 >> 1);
             const int off = (c4 & 1) * 4;
-            s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(sv + ka * D + ((ch ^ (ka & SWZ)) << 3) + off));
-            s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(sv + kb * D + ((ch ^ (kb & SWZ)) << 3) + off));
-            u32x2 l2 = __builtin_bit_cast(u32x2, lo4);
-            u32x2 h2 = __builtin_bit_cast(u32x2, hi4);
-            u32x4 av = {l2[0], l2[1], h2[0], h2[1]};
-            oacc[db] = mfma16x16x32<DT>(av, pk, oacc[db] * alpha);
+            f32x4 o = oacc[db] * alpha;
+#pragma unroll
+            for (int k2 = 0; k2 < NH / 2; ++k2) {
+                const int ka = 32 * k2 + 4 * G + r4, kb = ka + 16;
+                s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(sv + ka * D + (C::vswz(ka, ch) << 3) + off));
+                s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(sv + kb * D + (C::vswz(kb, ch) << 3) + off));
+                u32x2 l2 = __builtin_bit_cast(u32x2, lo4);
+                u32x2 h2 = __builtin_bit_cast(u32x2, hi4);
+                u32x4 av = {l2[0], l2[1], h2[0], h2[1]};
+                o = mfma16x16x32<DT>(av, pk[k2], o);
+            }
+            oacc[db] = o;
         }
     };
 
@@ -450,7 +475,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
 // LDS. (Merging inside the decode kernel, by the last wave to finish a
 // segment, was measured 1.6x slower: every partial then needs a device-scope
 // fence, i.e. an L2 write-back across the 8 XCDs.)
-template <int DT>
+template <int DT, int D>
 __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int workers) {
     using namespace dec;
     __shared__ __attribute__((aligned(16))) float s_acc[256][8];
@@ -559,45 +584,60 @@ constexpr int kDecodeStages = 3;
 
 int decode_workers(int cus) { return cus * dec::NWAVE; }
 
-template <int DT, int LAYOUT>
+template <int DT, int HD, int LAYOUT>
 static void launch_decode_l(const FwdArgs& a, int grid, hipStream_t stream) {
     const bool bias = a.softcap > 0.f || a.alibi != nullptr;
     const bool fuse = a.k_new != nullptr;
+    constexpr int S = kDecodeStages;
     if (bias) {
-        if (fuse) hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, true, true, LAYOUT>), dim3(grid), dim3(256), 0, stream, a);
-        else hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, true, false, LAYOUT>), dim3(grid), dim3(256), 0, stream, a);
+        if (fuse) hipLaunchKernelGGL((fa_decode_kernel<DT, HD, S, true, true, LAYOUT>), dim3(grid), dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((fa_decode_kernel<DT, HD, S, true, false, LAYOUT>), dim3(grid), dim3(256), 0, stream, a);
     } else {
-        if (fuse) hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, false, true, LAYOUT>), dim3(grid), dim3(256), 0, stream, a);
-        else hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, false, false, LAYOUT>), dim3(grid), dim3(256), 0, stream, a);
+        if (fuse) hipLaunchKernelGGL((fa_decode_kernel<DT, HD, S, false, true, LAYOUT>), dim3(grid), dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((fa_decode_kernel<DT, HD, S, false, false, LAYOUT>), dim3(grid), dim3(256), 0, stream, a);
     }
 }
 
-template <int DT>
+template <int DT, int HD>
 static void launch_decode_t(const FwdArgs& a, int grid, hipStream_t stream) {
-    if (a.hd < dec::D) {
-        // head dims below 128: the generic-layout, bias-capable instances
-        // with dim masking (correct for every input of this kernel)
-        if (a.k_new) hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, true, true, 2, true>), dim3(grid), dim3(256), 0, stream, a);
-        else hipLaunchKernelGGL((fa_decode_kernel<DT, kDecodeStages, true, false, 2, true>), dim3(grid), dim3(256), 0, stream, a);
+    constexpr int KT = DecCfg<HD>::KT;
+    if (a.hd < HD) {
+        // head dims below the kernel's: the generic-layout, bias-capable
+        // instances with dim masking (correct for every input of this kernel)
+        constexpr int S = kDecodeStages;
+        if (a.k_new) hipLaunchKernelGGL((fa_decode_kernel<DT, HD, S, true, true, 2, true>), dim3(grid), dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((fa_decode_kernel<DT, HD, S, true, false, 2, true>), dim3(grid), dim3(256), 0, stream, a);
         return;
     }
-    if (a.block_table && (a.page % dec::KT) == 0) launch_decode_l<DT, 1>(a, grid, stream);
-    else if (a.block_table || a.cu_seqlens_k) launch_decode_l<DT, 2>(a, grid, stream);
-    else launch_decode_l<DT, 0>(a, grid, stream);
+    if (a.block_table && (a.page % KT) == 0) launch_decode_l<DT, HD, 1>(a, grid, stream);
+    else if (a.block_table || a.cu_seqlens_k) launch_decode_l<DT, HD, 2>(a, grid, stream);
+    else launch_decode_l<DT, HD, 0>(a, grid, stream);
 }
 
-hipError_t launch_decode(const FwdArgs& a, int dtype, int grid, hipStream_t stream) {
-    if (dtype == DT_BF16) launch_decode_t<DT_BF16>(a, grid, stream);
-    else launch_decode_t<DT_FP16>(a, grid, stream);
+// d: the kernel head dim, 64 or 128 (a.hd <= d is the head dim in memory)
+hipError_t launch_decode(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream) {
+    if (d != 64 && d != 128) return hipErrorInvalidValue;
+    if (dtype == DT_BF16) {
+        if (d == 64) launch_decode_t<DT_BF16, 64>(a, grid, stream);
+        else launch_decode_t<DT_BF16, 128>(a, grid, stream);
+    } else {
+        if (d == 64) launch_decode_t<DT_FP16, 64>(a, grid, stream);
+        else launch_decode_t<DT_FP16, 128>(a, grid, stream);
+    }
     return hipGetLastError();
 }
 
-hipError_t launch_decode_merge(const FwdArgs& a, int dtype, int grid, hipStream_t stream) {
+hipError_t launch_decode_merge(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream) {
+    if (d != 64 && d != 128) return hipErrorInvalidValue;
     const int segs = a.B * a.Hk * 4;  // DSPLIT workgroups per (sequence, kv head) segment
-    if (dtype == DT_BF16)
-        hipLaunchKernelGGL(fa_decode_merge_kernel<DT_BF16>, dim3(segs), dim3(256), 0, stream, a, grid * dec::NWAVE);
-    else
-        hipLaunchKernelGGL(fa_decode_merge_kernel<DT_FP16>, dim3(segs), dim3(256), 0, stream, a, grid * dec::NWAVE);
+    const int w = grid * dec::NWAVE;
+    if (dtype == DT_BF16) {
+        if (d == 64) hipLaunchKernelGGL((fa_decode_merge_kernel<DT_BF16, 64>), dim3(segs), dim3(256), 0, stream, a, w);
+        else hipLaunchKernelGGL((fa_decode_merge_kernel<DT_BF16, 128>), dim3(segs), dim3(256), 0, stream, a, w);
+    } else {
+        if (d == 64) hipLaunchKernelGGL((fa_decode_merge_kernel<DT_FP16, 64>), dim3(segs), dim3(256), 0, stream, a, w);
+        else hipLaunchKernelGGL((fa_decode_merge_kernel<DT_FP16, 128>), dim3(segs), dim3(256), 0, stream, a, w);
+    }
     return hipGetLastError();
 }
 

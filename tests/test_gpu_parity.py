@@ -236,6 +236,22 @@ def test_headdim64_paged_chunked_prefill_rotary():
                 seed=76)
 
 
+# ---- decode at head dims up to 64: 64-key tiles, 128-byte LDS rows ----------------------------
+@pytest.mark.parametrize("D,page", [(64, 32), (32, 128), (48, 0), (64, 0)])
+def test_headdim64_decode_layouts(D, page):
+    print(f"case headdim64 decode D={D} page={page}", flush=True)
+    rng = np.random.default_rng(80 + D + page)
+    run_kvcache(6, 1, 32, 8, D, torch.bfloat16, 0 if page else 3000, rng.integers(1, 2900, size=6), s_new=1,
+                page=page, causal=True, seed=80 + D + page)
+
+
+def test_headdim64_decode_verify_window_alibi_softcap():
+    print("case headdim64 decode verify window alibi softcap", flush=True)
+    rng = np.random.default_rng(84)
+    run_kvcache(4, 4, 16, 4, 64, torch.float16, 0, rng.integers(700, 5000, size=4), s_new=4, page=64, causal=True,
+                window=(500, 0), alibi=True, softcap=30.0, batch_idx=True, seed=84)
+
+
 # ---- head dims above 128: the 256 prefill kernel (decode shapes run on it too) --------------
 @pytest.mark.parametrize("D", [136, 192, 256])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
