@@ -568,7 +568,8 @@ fa_status_t run_backward(const fa_bwd_params* p, int kind, void* stream_v) {
     a.wl = wl;
     a.wr = wr;
     a.chunk = p->attention_chunk;
-    const int kd = p->headdim <= 128 ? 128 : 256;  // kernel head dim; dims above headdim read as zero
+    // kernel head dim (64, 128 or 256); dims above headdim read as zero
+    const int kd = p->headdim <= 64 ? 64 : p->headdim <= 128 ? 128 : 256;
     const int64_t gkv = (int64_t)p->batch * p->nheads_k * ((p->seqlen_k + fa::bwd_key_block(kd) - 1) / fa::bwd_key_block(kd));
     const int64_t gq = (int64_t)p->batch * p->nheads_k *
                        (((int64_t)p->seqlen_q * a.g + fa::bwd_row_block(kd) - 1) / fa::bwd_row_block(kd));

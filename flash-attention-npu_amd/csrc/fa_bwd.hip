@@ -52,7 +52,7 @@ struct BwCfg {
 #define BW_KNW 8
 #endif
     static constexpr int KNW = HD > 128 ? 4 : BW_KNW;
-    static constexpr int KRB = HD > 128 ? 1 : BW_KRB;  // 16-key blocks per wave
+    static constexpr int KRB = HD > 128 ? 1 : HD == 64 ? 2 : BW_KRB;  // 16-key blocks per wave
     static constexpr int KNT = KNW * 64;
     static constexpr int BK = KNW * 16 * KRB;
     static constexpr int BQ = 64;
@@ -62,7 +62,7 @@ struct BwCfg {
     // 128, one wave per SIMD and 32-key tiles at 256
     static constexpr int QNW = HD > 128 ? 4 : 8;
     static constexpr int QNT = QNW * 64;
-    static constexpr int RB = 1;
+    static constexpr int RB = HD == 64 ? 2 : 1;
     static constexpr int BM = QNW * RB * 16;
     static constexpr int BN = HD > 128 ? 32 : 64;
     static constexpr int CPK = BN * DCH / QNT;
@@ -185,6 +185,9 @@ __global__ void __launch_bounds__(256) fa_bwd_dsum_kernel(BwdArgs a, int dt) {
 // ---- dK, dV ---------------------------------------------------------------------------------
 template <int DT, int HD, bool BIAS, bool CHUNK>
 __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs a) {
+    // LDS swizzles for the row length (128-byte rows at head dim 64)
+    auto tv = [](int r, int c) { return HD == 64 ? swz_b64(r, c) : swz_v(r, c); };  // row and transpose reads
+    auto tk = [](int r, int c) { return HD == 64 ? swz_k64(r, c) : swz_k(r, c); };  // row reads
     using C = BwCfg<HD>;
     constexpr int D = C::D, DCH = C::DCH, KSTEPS = C::KSTEPS, DBLK = C::DBLK, BK = C::BK, BQ = C::BQ,
                   CPQ = C::CPQ, NT = C::KNT, KRB = C::KRB;
@@ -204,15 +207,15 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
     });
 
     // LDS offsets: row reads (A operands) and transpose reads, both on the
-    // swz_v layout; staging stores
+    // tv layout; staging stores
     int offr[KSTEPS];
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) offr[s] = li * D + (swz_v(li, G * KSTEPS + s) << 3);
+    for (int s = 0; s < KSTEPS; ++s) offr[s] = li * D + (tv(li, G * KSTEPS + s) << 3);
     const int r4 = li >> 2, c4 = li & 3;
     int offt[DBLK];
 #pragma unroll
     for (int db = 0; db < DBLK; ++db)
-        offt[db] = (4 * G + r4) * D + (swz_v(4 * G + r4, 2 * db + (c4 >> 1)) << 3) + (c4 & 1) * 4;
+        offt[db] = (4 * G + r4) * D + (tv(4 * G + r4, 2 * db + (c4 >> 1)) << 3) + (c4 & 1) * 4;
     const int dch = tid % DCH, rr0 = tid / DCH;
 
     const uint16_t* qp = static_cast<const uint16_t*>(a.q);
@@ -332,7 +335,7 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
 #pragma unroll
             for (int u = 0; u < CPQ; ++u) {
                 const int r = rr0 + u * (NT / DCH);
-                const int off = r * D + (swz_v(r, dch) << 3);
+                const int off = r * D + (tv(r, dch) << 3);
                 *reinterpret_cast<u32x4*>(&s_q[buf][off]) = qr[u];
                 *reinterpret_cast<u32x4*>(&s_do[buf][off]) = dr[u];
             }
@@ -501,11 +504,14 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
 // ---- dQ -------------------------------------------------------------------------------------
 template <int DT, int HD, bool BIAS>
 __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a) {
+    // LDS swizzles for the row length (128-byte rows at head dim 64)
+    auto tv = [](int r, int c) { return HD == 64 ? swz_b64(r, c) : swz_v(r, c); };  // row and transpose reads
+    auto tk = [](int r, int c) { return HD == 64 ? swz_k64(r, c) : swz_k(r, c); };  // row reads
     using C = BwCfg<HD>;
     constexpr int D = C::D, DCH = C::DCH, KSTEPS = C::KSTEPS, DBLK = C::DBLK, RB = C::RB, BM = C::BM, BN = C::BN,
                   CPK = C::CPK, NT = C::QNT;
-    __shared__ __attribute__((aligned(16))) uint16_t s_k[2][BN * D];  // swz_v: row reads and transpose reads
-    __shared__ __attribute__((aligned(16))) uint16_t s_v[2][BN * D];  // swz_k: row reads
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[2][BN * D];  // tv: row reads and transpose reads
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[2][BN * D];  // tk: row reads
     __shared__ int s_pref[bw::kMaxBatch + 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -518,14 +524,14 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
     int offkr[KSTEPS], offvr[KSTEPS];
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
-        offkr[s] = li * D + (swz_v(li, G * KSTEPS + s) << 3);
-        offvr[s] = li * D + (swz_k(li, G * KSTEPS + s) << 3);
+        offkr[s] = li * D + (tv(li, G * KSTEPS + s) << 3);
+        offvr[s] = li * D + (tk(li, G * KSTEPS + s) << 3);
     }
     const int r4 = li >> 2, c4 = li & 3;
     int offt[DBLK];
 #pragma unroll
     for (int db = 0; db < DBLK; ++db)
-        offt[db] = (4 * G + r4) * D + (swz_v(4 * G + r4, 2 * db + (c4 >> 1)) << 3) + (c4 & 1) * 4;
+        offt[db] = (4 * G + r4) * D + (tv(4 * G + r4, 2 * db + (c4 >> 1)) << 3) + (c4 & 1) * 4;
     const int dch = tid % DCH, kk0 = tid / DCH;
 
     const uint16_t* qp = static_cast<const uint16_t*>(a.q);
@@ -619,8 +625,8 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
 #pragma unroll
             for (int u = 0; u < CPK; ++u) {
                 const int r = kk0 + u * (NT / DCH);
-                *reinterpret_cast<u32x4*>(&s_k[buf][r * D + (swz_v(r, dch) << 3)]) = kr[u];
-                *reinterpret_cast<u32x4*>(&s_v[buf][r * D + (swz_k(r, dch) << 3)]) = vr[u];
+                *reinterpret_cast<u32x4*>(&s_k[buf][r * D + (tv(r, dch) << 3)]) = kr[u];
+                *reinterpret_cast<u32x4*>(&s_v[buf][r * D + (tk(r, dch) << 3)]) = vr[u];
             }
         };
 
@@ -757,19 +763,20 @@ static void launch_bwd_d(const BwdArgs& a, int dtype, int grid_kv, int grid_q, h
     }
 }
 
-int bwd_key_block(int d) { return d > 128 ? BwCfg<256>::BK : BwCfg<128>::BK; }
-int bwd_row_block(int d) { return d > 128 ? BwCfg<256>::BM : BwCfg<128>::BM; }
+int bwd_key_block(int d) { return d > 128 ? BwCfg<256>::BK : d > 64 ? BwCfg<128>::BK : BwCfg<64>::BK; }
+int bwd_row_block(int d) { return d > 128 ? BwCfg<256>::BM : d > 64 ? BwCfg<128>::BM : BwCfg<64>::BM; }
 
 // d: kernel head dim (128 or 256); grids: upper bounds on the work items of each kernel
 hipError_t launch_bwd(const BwdArgs& a, int dtype, int d, int grid_kv, int grid_q, hipStream_t stream) {
-    if (d != 128 && d != 256) return hipErrorInvalidValue;
+    if (d != 64 && d != 128 && d != 256) return hipErrorInvalidValue;
     const int64_t ntok = a.cu_seqlens_q ? (int64_t)a.total_q : (int64_t)a.B * a.Sq;
     const int64_t rows = ntok * a.H;
     if (rows > 0) {
         const int64_t gsum = (rows + 15) / 16;
         hipLaunchKernelGGL(fa_bwd_dsum_kernel, dim3((unsigned)gsum), dim3(256), 0, stream, a, dtype);
     }
-    if (d == 128) launch_bwd_d<128>(a, dtype, grid_kv, grid_q, stream);
+    if (d == 64) launch_bwd_d<64>(a, dtype, grid_kv, grid_q, stream);
+    else if (d == 128) launch_bwd_d<128>(a, dtype, grid_kv, grid_q, stream);
     else launch_bwd_d<256>(a, dtype, grid_kv, grid_q, stream);
     return hipGetLastError();
 }

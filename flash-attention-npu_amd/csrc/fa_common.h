@@ -73,6 +73,14 @@ __device__ __forceinline__ int swz_v(int r, int c) { return c ^ ((r & 3) << 1) ^
 // a half wave of transpose reads covers take 4 disjoint chunk pairs per parity.
 __device__ __forceinline__ int swz_k64(int r, int c) { return c ^ ((r >> 1) & 7); }
 __device__ __forceinline__ int swz_v64(int r, int c) { return c ^ (((r >> 1) & 3) << 1); }
+// 128-byte rows read both ways (row reads of 16 rows and transpose reads of 8
+// rows by a half wave): the XOR f(x) = ((x & 3) << 1) | (x >> 2) of x = r >> 1
+// is a bijection on 0..7 (16 distinct 4-bank groups for a row read) and gives
+// rows 0..7 chunk pairs 0, 2, 4, 6 apart (disjoint for a transpose read).
+__device__ __forceinline__ int swz_b64(int r, int c) {
+    const int x = (r >> 1) & 7;
+    return c ^ (((x & 3) << 1) | (x >> 2));
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }

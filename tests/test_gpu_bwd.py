@@ -194,6 +194,20 @@ def test_bwd_headdim_64_gqa_causal():
     run_dense(torch.float16, 2, 8, 2, 300, 300, 64, True, seed=12)
 
 
+# head dims up to 64 run the 64 backward kernels (32 keys per dK/dV wave, 32 rows per dQ wave)
+@pytest.mark.parametrize("D", [32, 48, 64])
+def test_bwd_headdim64_noncausal(D):
+    run_dense(torch.bfloat16, 2, 4, 4, 333, 270, D, False, seed=20 + D)
+
+
+def test_bwd_headdim64_window_softcap_alibi():
+    run_dense(torch.bfloat16, 2, 8, 4, 400, 512, 64, True, window=(120, 0), softcap=25.0, alibi=True, seed=21)
+
+
+def test_bwd_headdim64_varlen():
+    run_varlen(torch.float16, 8, 2, [129, 1, 500, 64], [200, 33, 500, 64], 64, True, seed=22)
+
+
 def test_bwd_v3_api():
     run_dense(torch.bfloat16, 2, 4, 2, 256, 384, 128, True, api="v3", seed=13)
     run_varlen(torch.bfloat16, 4, 2, [50, 200], [60, 260], 128, True, api="v3", seed=14)
