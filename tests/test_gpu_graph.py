@@ -110,3 +110,57 @@ def test_graph_dense_split():
     eager = [t.clone() for t in fn()]
     torch.cuda.synchronize()
     _replay_and_check(fn, eager)
+
+
+def test_graph_v3_ragged_kvcache_leftpad_chunk():
+    """The v3 operator with ragged queries and new tokens, cache_leftpad,
+    rotary_seqlens and attention_chunk: a serving step captured once."""
+    import flash_attn_npu_v3
+    print("case graph v3 ragged kvcache", flush=True)
+    g = torch.Generator().manual_seed(73)
+    H, Hk, D, cap = 16, 4, 128, 1024
+    q_lens, new_lens = [1, 40, 3], [1, 40, 3]
+    cu_q = torch.tensor([0, 1, 41, 44], dtype=torch.int32, device=DEV)
+    cu_n = torch.tensor([0, 1, 41, 44], dtype=torch.int32, device=DEV)
+    q = _randn((sum(q_lens), H, D), torch.bfloat16, g)
+    kn = _randn((sum(new_lens), Hk, D), torch.bfloat16, g)
+    vn = _randn((sum(new_lens), Hk, D), torch.bfloat16, g)
+    kc = _randn((3, cap, Hk, D), torch.bfloat16, g)
+    vc = _randn((3, cap, Hk, D), torch.bfloat16, g)
+    inv = 1.0 / (10000 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    ang = torch.arange(2048, dtype=torch.float32)[:, None] * inv[None, :]
+    cos, sin = torch.cos(ang).to(torch.bfloat16).to(DEV), torch.sin(ang).to(torch.bfloat16).to(DEV)
+    seqlens = torch.tensor([500, 0, 900], dtype=torch.int32, device=DEV)
+    leftpad = torch.tensor([100, 0, 7], dtype=torch.int32, device=DEV)
+    rot = torch.tensor([400, 0, 893], dtype=torch.int32, device=DEV)
+
+    def fn():
+        out, lse, *_ = flash_attn_npu_v3.flash_attn_with_kvcache(
+            q, kc, vc, k=kn, v=vn, rotary_cos=cos, rotary_sin=sin, cache_seqlens=seqlens, cache_leftpad=leftpad,
+            cu_seqlens_q=cu_q, cu_seqlens_k_new=cu_n, max_seqlen_q=40, rotary_seqlens=rot, causal=True,
+            attention_chunk=256, rotary_interleaved=False, return_softmax_lse=True)
+        return out, lse
+
+    eager = [t.clone() for t in fn()]
+    torch.cuda.synchronize()
+    _replay_and_check(fn, eager)
+
+
+def test_graph_backward():
+    """Forward and backward of flash_attn_func captured together (a training step)."""
+    import flash_attn_npu_v2
+    print("case graph backward", flush=True)
+    g = torch.Generator().manual_seed(74)
+    q = _randn((2, 300, 8, 128), torch.bfloat16, g).requires_grad_(True)
+    k = _randn((2, 300, 2, 128), torch.bfloat16, g).requires_grad_(True)
+    v = _randn((2, 300, 2, 128), torch.bfloat16, g).requires_grad_(True)
+    do = _randn((2, 300, 8, 128), torch.bfloat16, g)
+
+    def fn():
+        out = flash_attn_npu_v2.flash_attn_func(q, k, v, causal=True)
+        dq, dk, dv = torch.autograd.grad(out, (q, k, v), do)
+        return out.detach(), dq, dk, dv
+
+    eager = [t.clone() for t in fn()]
+    torch.cuda.synchronize()
+    _replay_and_check(fn, eager)
