@@ -75,6 +75,7 @@ int cu_count() {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool strides8(int64_t a, int64_t b, int64_t c) { return (a % 8) == 0 && (b % 8) == 0 && (c % 8) == 0; }
+bool strides16(int64_t a, int64_t b, int64_t c) { return (a % 16) == 0 && (b % 16) == 0 && (c % 16) == 0; }
 
 struct Plan {
     bool decode;
@@ -101,10 +102,24 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
     FA_CHECK(p->abi_version == FA_MI355X_ABI_VERSION, "abi_version %d does not match library ABI %d", p->abi_version,
              FA_MI355X_ABI_VERSION);
     FA_CHECK(kind == FA_KIND_KVCACHE || kind == FA_KIND_DENSE || kind == FA_KIND_VARLEN, "unknown kind %d", kind);
-    FA_CHECK(p->dtype == FA_DTYPE_FP16 || p->dtype == FA_DTYPE_BF16,
-             "FlashAttention only support fp16 and bf16 data type");
+    const bool f8 = p->dtype == FA_DTYPE_FP8_E4M3;
+    FA_CHECK(p->dtype == FA_DTYPE_FP16 || p->dtype == FA_DTYPE_BF16 || f8,
+             "FlashAttention only support fp16 and bf16 data type (and fp8 e4m3 inputs in the forward)");
     FA_CHECK(p->batch >= 1, "batch size must be positive");
     FA_CHECK(p->batch <= kMaxBatch, "batch size %d exceeds the supported maximum %d", p->batch, kMaxBatch);
+    if (f8) {
+        // 16-byte loads of e4m3 rows: 16-element head-dim chunks and row starts
+        FA_CHECK(p->headdim % 16 == 0, "FP8 inputs need a head dimension that is a multiple of 16");
+        FA_CHECK(strides16(p->q_batch_stride, p->q_row_stride, p->q_head_stride) &&
+                     strides16(p->k_batch_stride, p->k_row_stride, p->k_head_stride) &&
+                     strides16(p->v_batch_stride, p->v_row_stride, p->v_head_stride),
+                 "FP8 q, k and v strides must be multiples of 16 elements");
+        FA_CHECK(p->rotary_cos == nullptr && p->rotary_sin == nullptr, "rotary is not supported with FP8 inputs");
+        if (p->k_new)
+            FA_CHECK(strides16(p->knew_batch_stride, p->knew_row_stride, p->knew_head_stride) &&
+                         strides16(p->vnew_batch_stride, p->vnew_row_stride, p->vnew_head_stride),
+                     "FP8 k and v strides must be multiples of 16 elements");
+    }
     FA_CHECK(p->nheads >= 1 && p->nheads_k >= 1, "number of heads must be positive");
     FA_CHECK(p->nheads % p->nheads_k == 0, "Number of heads in key/value must divide number of heads in query");
     FA_CHECK(p->headdim >= 1, "head dimension must be positive");
@@ -392,6 +407,17 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
         a.rot_pos = pl.rotary ? p->rotary_seqlens : nullptr;
     }
     a.chunk = p->attention_chunk;
+    if (p->dtype == FA_DTYPE_FP8_E4M3) {  // descales are read for FP8 inputs only
+        a.qd = p->q_descale;
+        a.qd_sb = p->q_descale_batch_stride;
+        a.qd_sh = p->q_descale_head_stride;
+        a.kd = p->k_descale;
+        a.kd_sb = p->k_descale_batch_stride;
+        a.kd_sh = p->k_descale_head_stride;
+        a.vd = p->v_descale;
+        a.vd_sb = p->v_descale_batch_stride;
+        a.vd_sh = p->v_descale_head_stride;
+    }
     if (fused_append) {
         a.k_new = p->k_new;
         a.kn_sb = p->knew_batch_stride;

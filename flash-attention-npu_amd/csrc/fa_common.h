@@ -5,7 +5,9 @@
 
 namespace fa {
 
-enum : int { DT_FP16 = 0, DT_BF16 = 1 };
+// DT_FP8: OCP e4m3fn inputs, widened to bf16 on load; bf16 arithmetic and
+// output (the value matches FA_DTYPE_FP8_E4M3).
+enum : int { DT_FP16 = 0, DT_BF16 = 1, DT_FP8 = 3 };
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -21,45 +23,65 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 // 16x16x32 MFMA on 16-byte packed operands. Lane l holds A[l%16][8*(l/16)+e]
 // and B[8*(l/16)+e][l%16]; the result lane l holds D[4*(l/16)+i][l%16].
+// DT_FP8 operands are already widened to bf16.
 template <int DT>
 __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
-    if constexpr (DT == DT_BF16) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-    } else {
+    if constexpr (DT == DT_FP16) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                       __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
     }
 }
 
-// Round-to-nearest-even conversions of 8 floats into one 16-byte operand.
+// Round-to-nearest-even conversions of 8 floats into one 16-byte operand
+// (bf16 for DT_BF16 and DT_FP8).
 template <int DT>
 __device__ __forceinline__ u32x4 pack8(f32x8 v) {
-    if constexpr (DT == DT_BF16) {
-        bf16x8 h = __builtin_convertvector(v, bf16x8);
+    if constexpr (DT == DT_FP16) {
+        f16x8 h = __builtin_convertvector(v, f16x8);
         return __builtin_bit_cast(u32x4, h);
     } else {
-        f16x8 h = __builtin_convertvector(v, f16x8);
+        bf16x8 h = __builtin_convertvector(v, bf16x8);
         return __builtin_bit_cast(u32x4, h);
     }
 }
 
 template <int DT>
 __device__ __forceinline__ uint16_t f32_to_16(float f) {
-    if constexpr (DT == DT_BF16) {
-        return __builtin_bit_cast(uint16_t, (__bf16)f);
-    } else {
+    if constexpr (DT == DT_FP16) {
         return __builtin_bit_cast(uint16_t, (_Float16)f);
+    } else {
+        return __builtin_bit_cast(uint16_t, (__bf16)f);
     }
 }
 
 template <int DT>
 __device__ __forceinline__ float f16_to_32(uint16_t h) {
-    if constexpr (DT == DT_BF16) {
-        return __builtin_bit_cast(float, (uint32_t)h << 16);
-    } else {
+    if constexpr (DT == DT_FP16) {
         return (float)__builtin_bit_cast(_Float16, h);
+    } else {
+        return __builtin_bit_cast(float, (uint32_t)h << 16);
     }
+}
+
+// 8 e4m3fn values (the bytes of r, lowest first) -> 8 bf16 in one 16-byte
+// operand. Exact: every e4m3fn value (normal, subnormal, +-0, NaN) is a bf16
+// value, and the scale is 1.
+__device__ __forceinline__ u32x4 fp8x8_to_bf16(u32x2 r) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    u32x4 o;
+    o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)r[0], 1.0f, false));
+    o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)r[0], 1.0f, true));
+    o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)r[1], 1.0f, false));
+    o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)r[1], 1.0f, true));
+    return o;
+}
+
+// FP8 descale factor of (batch b, kv head hk); a null table means 1.
+__device__ __forceinline__ float descale_at(const float* p, int64_t sb, int64_t sh, int b, int hk) {
+    return p ? p[(int64_t)b * sb + (int64_t)hk * sh] : 1.f;
 }
 
 // LDS tile swizzles (16-byte chunk c of row r): swz_k keeps 16 consecutive

@@ -22,6 +22,8 @@
 #include "fa_common.h"
 #include "fa_kernel_args.h"
 
+#include <type_traits>
+
 namespace fa {
 namespace dec {
 constexpr int NWAVE = 4;     // waves (workers) per workgroup
@@ -102,11 +104,19 @@ __device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref
 // BIAS: softcap or ALiBi present; FUSE: append k_new/v_new in this kernel;
 // LAYOUT: 0 = batch-strided cache, 1 = paged with page % 32 == 0, 2 = any;
 // HDM: head dim below 128 (dims >= a.hd read as zero, never written).
+// DT_FP8: the cache, q and k_new / v_new hold e4m3fn bytes. The register
+// pipeline carries the raw bytes (half the registers and half the HBM bytes
+// of a bf16 cache); a tile is widened to bf16 when it is consumed, and the
+// descales scale the scores (q_descale * k_descale) and the output (v_descale).
 template <int DT, int HD, int STAGES, bool BIAS, bool FUSE, int LAYOUT, bool HDM = false>
 __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     using namespace dec;
     using C = DecCfg<HD>;
     constexpr int D = C::D, KT = C::KT, NH = C::NH, KSTEPS = C::KSTEPS, DBLK = C::DBLK;
+    constexpr bool F8 = DT == DT_FP8;
+    using ET = std::conditional_t<F8, uint8_t, uint16_t>;  // stored element
+    constexpr int EPL = 16 / sizeof(ET);                    // elements per 16-byte load
+    constexpr int KL = F8 ? KSTEPS / 2 : KSTEPS;            // 16-byte loads per lane and key row
     __shared__ int s_pref[MAXB + 1];
     __shared__ DecBatch s_bat[MAXB];
     __shared__ int s_tab[NWAVE][TABN];
@@ -153,9 +163,9 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     const int t0 = (int)(wid * T / W), t1 = (int)((wid + 1) * T / W);
     if (t0 >= t1) return;  // no block barrier follows: waves are independent from here
 
-    const uint16_t* qp = static_cast<const uint16_t*>(a.q);
-    const uint16_t* kp = static_cast<const uint16_t*>(a.k);
-    const uint16_t* vp = static_cast<const uint16_t*>(a.v);
+    const ET* qp = static_cast<const ET*>(a.q);
+    const ET* kp = static_cast<const ET*>(a.k);
+    const ET* vp = static_cast<const ET*>(a.v);
     uint16_t* sv = s_v[wave];
     int* tab = s_tab[wave];
     const bool paged = LAYOUT == 1 || (LAYOUT == 2 && a.block_table != nullptr);
@@ -179,12 +189,12 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     if (tab_ok) fill_tab(tab_base);
 
     // ---- issue side: STAGES-deep register pipeline ------------------------------------
-    u32x4 kr[STAGES][NH][KSTEPS], vr[STAGES][NH][KSTEPS];
+    u32x4 kr[STAGES][NH][KL], vr[STAGES][NH][KL];
     int bk[STAGES];  // paged block id of each in-flight tile
     DecSeg is = dec_seg_of(a, s_pref, s_bat, t0);
 
-    auto row_ptr = [&](const uint16_t* base, int64_t sb, int64_t si, int64_t sh, const DecSeg& s, int key,
-                       int blk) -> const uint16_t* {
+    auto row_ptr = [&](const ET* base, int64_t sb, int64_t si, int64_t sh, const DecSeg& s, int key,
+                       int blk) -> const ET* {
         if (paged) {
             int b2 = blk;
             if (!tab_ok) {
@@ -202,10 +212,10 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     // worker that owns their tile also writes them into the cache (each tile
     // has exactly one owner, and no other tile reads those positions).
     constexpr bool fuse = FUSE;
-    const uint16_t* knp = static_cast<const uint16_t*>(a.k_new);
-    const uint16_t* vnp = static_cast<const uint16_t*>(a.v_new);
+    const ET* knp = static_cast<const ET*>(a.k_new);
+    const ET* vnp = static_cast<const ET*>(a.v_new);
 
-    auto issue = [&](int t, u32x4 (&kk)[NH][KSTEPS], u32x4 (&vv)[NH][KSTEPS], int& blk) {
+    auto issue = [&](int t, u32x4 (&kk)[NH][KL], u32x4 (&vv)[NH][KL], int& blk) {
         if (t >= t1) return;
         if (t >= is.S + is.n) is = dec_seg_of(a, s_pref, s_bat, t);
         blk = 0;
@@ -222,8 +232,8 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         for (int h = 0; h < NH; ++h) {
             const int key = key0 + h * 16 + li;
             if (key < is.sk) {
-                const uint16_t* kpr;
-                const uint16_t* vpr;
+                const ET* kpr;
+                const ET* vpr;
                 if (key >= first_new) {
                     const int tn = key - first_new;
                     kpr = knp + (int64_t)is.b * a.kn_sb + (int64_t)tn * a.kn_si + (int64_t)is.hk * a.kn_sh + G * (D / 4);
@@ -233,14 +243,14 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                     vpr = row_ptr(vp, a.v_sb, a.v_si, a.v_sh, is, key, blk) + G * (D / 4);
                 }
 #pragma unroll
-                for (int s = 0; s < KSTEPS; ++s) {
-                    const bool in = !HDM || G * (D / 4) + s * 8 < a.hd;
-                    kk[h][s] = in ? *reinterpret_cast<const u32x4*>(kpr + s * 8) : u32x4{0u, 0u, 0u, 0u};
-                    vv[h][s] = in ? *reinterpret_cast<const u32x4*>(vpr + s * 8) : u32x4{0u, 0u, 0u, 0u};
+                for (int s = 0; s < KL; ++s) {
+                    const bool in = !HDM || G * (D / 4) + s * EPL < a.hd;
+                    kk[h][s] = in ? *reinterpret_cast<const u32x4*>(kpr + s * EPL) : u32x4{0u, 0u, 0u, 0u};
+                    vv[h][s] = in ? *reinterpret_cast<const u32x4*>(vpr + s * EPL) : u32x4{0u, 0u, 0u, 0u};
                 }
             } else {
 #pragma unroll
-                for (int s = 0; s < KSTEPS; ++s) {
+                for (int s = 0; s < KL; ++s) {
                     kk[h][s] = u32x4{0u, 0u, 0u, 0u};
                     vv[h][s] = u32x4{0u, 0u, 0u, 0u};
                 }
@@ -257,6 +267,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     float m_run, l_run;
     int rows = 0;
     int seg_flo = 0, seg_fhi = 0;  // keys visible to every row of the segment: [seg_flo, seg_fhi]
+    float sc_qk = a.scale, sc_qk2 = a.scale_log2, sc_v = 1.f;  // per segment (FP8 descales)
 
     auto begin_seg = [&](const DecSeg& s) {
         rows = s.sq * a.g;
@@ -267,13 +278,24 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         const int h = s.hk * a.g + (ok ? li % a.g : 0);
         qi = i;
         slope = (a.alibi && ok) ? a.alibi[(int64_t)s.b * a.alibi_sb + h] : 0.f;
-        const uint16_t* qrow = a.cu_seqlens_q
-                                   ? qp + ((int64_t)a.cu_seqlens_q[s.b] + i) * a.q_si + (int64_t)h * a.q_sh
-                                   : qp + (int64_t)s.b * a.q_sb + (int64_t)i * a.q_si + (int64_t)h * a.q_sh;
+        const ET* qrow = a.cu_seqlens_q
+                             ? qp + ((int64_t)a.cu_seqlens_q[s.b] + i) * a.q_si + (int64_t)h * a.q_sh
+                             : qp + (int64_t)s.b * a.q_sb + (int64_t)i * a.q_si + (int64_t)h * a.q_sh;
 #pragma unroll
-        for (int s2 = 0; s2 < KSTEPS; ++s2)
-            qreg[s2] = ok && (!HDM || (G * KSTEPS + s2) * 8 < a.hd) ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s2) * 8)
-                                                          : u32x4{0u, 0u, 0u, 0u};
+        for (int s2 = 0; s2 < KSTEPS; ++s2) {
+            const bool in = ok && (!HDM || (G * KSTEPS + s2) * 8 < a.hd);
+            if constexpr (F8)
+                qreg[s2] = in ? fp8x8_to_bf16(*reinterpret_cast<const u32x2*>(qrow + (G * KSTEPS + s2) * 8))
+                              : u32x4{0u, 0u, 0u, 0u};
+            else
+                qreg[s2] = in ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s2) * 8) : u32x4{0u, 0u, 0u, 0u};
+        }
+        if constexpr (F8) {
+            const float qk = descale_at(a.qd, a.qd_sb, a.qd_sh, s.b, s.hk) * descale_at(a.kd, a.kd_sb, a.kd_sh, s.b, s.hk);
+            sc_qk = a.scale * qk;
+            sc_qk2 = a.scale_log2 * qk;
+            sc_v = descale_at(a.vd, a.vd_sb, a.vd_sh, s.b, s.hk);
+        }
         m_run = -INFINITY;
         l_run = 0.f;
 #pragma unroll
@@ -283,7 +305,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     auto end_seg = [&](const DecSeg& s) {
         const float lrow = wave_sum16x4(l_run);
         const bool nonempty = lrow > 0.f;
-        const float inv = nonempty ? 1.f / lrow : 0.f;
+        const float inv = nonempty ? (F8 ? sc_v / lrow : 1.f / lrow) : 0.f;
         const bool whole = s.S >= t0 && s.S + s.n <= t1;
         if (li >= rows) return;
         if (whole) {
@@ -314,29 +336,38 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         }
     };
 
-    auto compute = [&](int t, const u32x4 (&kk)[NH][KSTEPS], const u32x4 (&vv)[NH][KSTEPS], int blk) {
+    auto compute = [&](int t, const u32x4 (&kk)[NH][KL], const u32x4 (&vv)[NH][KL], int blk) {
         const int key0 = (cs.lo_tile + (t - cs.S)) * KT;
         if (fuse && key0 + KT > cs.sk - a.seqlen_new) {
             // this tile holds appended tokens: write them into the cache
             const int first_new = cs.sk - a.seqlen_new;
-            uint16_t* kc = const_cast<uint16_t*>(kp);
-            uint16_t* vc = const_cast<uint16_t*>(vp);
+            ET* kc = const_cast<ET*>(kp);
+            ET* vc = const_cast<ET*>(vp);
 #pragma unroll
             for (int h = 0; h < NH; ++h) {
                 const int key = key0 + h * 16 + li;
                 if (key >= first_new && key < cs.sk) {
-                    uint16_t* kd = const_cast<uint16_t*>(row_ptr(kc, a.k_sb, a.k_si, a.k_sh, cs, key, blk)) + G * (D / 4);
-                    uint16_t* vd = const_cast<uint16_t*>(row_ptr(vc, a.v_sb, a.v_si, a.v_sh, cs, key, blk)) + G * (D / 4);
+                    ET* kd = const_cast<ET*>(row_ptr(kc, a.k_sb, a.k_si, a.k_sh, cs, key, blk)) + G * (D / 4);
+                    ET* vd = const_cast<ET*>(row_ptr(vc, a.v_sb, a.v_si, a.v_sh, cs, key, blk)) + G * (D / 4);
 #pragma unroll
-                    for (int s = 0; s < KSTEPS; ++s) {
-                        if (!HDM || G * (D / 4) + s * 8 < a.hd) {
-                            *reinterpret_cast<u32x4*>(kd + s * 8) = kk[h][s];
-                            *reinterpret_cast<u32x4*>(vd + s * 8) = vv[h][s];
+                    for (int s = 0; s < KL; ++s) {
+                        if (!HDM || G * (D / 4) + s * EPL < a.hd) {
+                            *reinterpret_cast<u32x4*>(kd + s * EPL) = kk[h][s];
+                            *reinterpret_cast<u32x4*>(vd + s * EPL) = vv[h][s];
                         }
                     }
                 }
             }
         }
+        // 16-byte bf16 / fp16 operand s of key block h (FP8: half of a raw load, widened)
+        auto opnd = [&](const u32x4 (&x)[NH][KL], int h, int s) -> u32x4 {
+            if constexpr (F8) {
+                const u32x4 r = x[h][s >> 1];
+                return fp8x8_to_bf16((s & 1) ? u32x2{r[2], r[3]} : u32x2{r[0], r[1]});
+            } else {
+                return x[h][s];
+            }
+        };
         // V tile -> wave-private LDS (row-major, 16-byte XOR swizzle)
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
@@ -344,7 +375,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s) {
                 const int ch = G * KSTEPS + s;
-                *reinterpret_cast<u32x4*>(sv + kl * D + (C::vswz(kl, ch) << 3)) = vv[h][s];
+                *reinterpret_cast<u32x4*>(sv + kl * D + (C::vswz(kl, ch) << 3)) = opnd(vv, h, s);
             }
         }
         // S^T = K . Q^T
@@ -354,7 +385,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
-            for (int h = 0; h < NH; ++h) sacc[h] = mfma16x16x32<DT>(kk[h][s], qreg[s], sacc[h]);
+            for (int h = 0; h < NH; ++h) sacc[h] = mfma16x16x32<DT>(opnd(kk, h, s), qreg[s], sacc[h]);
         // online softmax (log2 domain), row = li, keys key0 + 16h + 4G + e
         const int sk = cs.sk, diag0 = cs.sk - cs.sq;
         const bool full = key0 + KT <= sk && key0 >= seg_flo && key0 + KT - 1 <= seg_fhi;
@@ -367,9 +398,9 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                 const float sv2 = sacc[h][e];
                 float xv;
                 if (plain) {
-                    xv = sv2 * a.scale_log2;
+                    xv = sv2 * (F8 ? sc_qk2 : a.scale_log2);
                 } else {
-                    float y = sv2 * a.scale;
+                    float y = sv2 * (F8 ? sc_qk : a.scale);
                     if (a.softcap > 0.f) y = a.softcap * tanhf(y / a.softcap);
                     if (a.alibi) {
                         int dist = qi + diag0 - (key0 + h * 16 + G * 4 + e);
@@ -620,6 +651,9 @@ hipError_t launch_decode(const FwdArgs& a, int dtype, int d, int grid, hipStream
     if (dtype == DT_BF16) {
         if (d == 64) launch_decode_t<DT_BF16, 64>(a, grid, stream);
         else launch_decode_t<DT_BF16, 128>(a, grid, stream);
+    } else if (dtype == DT_FP8) {
+        if (d == 64) launch_decode_t<DT_FP8, 64>(a, grid, stream);
+        else launch_decode_t<DT_FP8, 128>(a, grid, stream);
     } else {
         if (d == 64) launch_decode_t<DT_FP16, 64>(a, grid, stream);
         else launch_decode_t<DT_FP16, 128>(a, grid, stream);
@@ -631,7 +665,7 @@ hipError_t launch_decode_merge(const FwdArgs& a, int dtype, int d, int grid, hip
     if (d != 64 && d != 128) return hipErrorInvalidValue;
     const int segs = a.B * a.Hk * 4;  // DSPLIT workgroups per (sequence, kv head) segment
     const int w = grid * dec::NWAVE;
-    if (dtype == DT_BF16) {
+    if (dtype == DT_BF16 || dtype == DT_FP8) {  // FP8 inputs give a bf16 output
         if (d == 64) hipLaunchKernelGGL((fa_decode_merge_kernel<DT_BF16, 64>), dim3(segs), dim3(256), 0, stream, a, w);
         else hipLaunchKernelGGL((fa_decode_merge_kernel<DT_BF16, 128>), dim3(segs), dim3(256), 0, stream, a, w);
     } else {

@@ -204,14 +204,21 @@ struct PfCfg {
 };
 
 
-// BIAS: softcap, ALiBi or a non-positive scale (scores are formed explicitly);
-// PAGED: K/V rows come through the block table; ROT: q is rotated (kvcache
-// rotary) as it is loaded.
+// BIAS: softcap, ALiBi, a non-positive scale or FP8 descales (scores are
+// formed explicitly); PAGED: K/V rows come through the block table; ROT: q is
+// rotated (kvcache rotary) as it is loaded. DT_FP8: q, K and V are e4m3fn
+// bytes, carried raw through the load registers and widened to bf16 on their
+// way into registers (q) and LDS (K/V tiles); the LDS tiles, the MFMAs and
+// the output are bf16.
 template <int DT, int HD, bool BIAS, bool PAGED, bool ROT>
 __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a) {
     using C = PfCfg<HD>;
     constexpr int D = C::D, RB = C::RB, NW = C::NW, NT = C::NT, BM = C::BM, BN = C::BN, DCH = C::DCH,
                   CPT = C::CPT, KSTEPS = C::KSTEPS, DBLK = C::DBLK, VPRE = C::VPRE;
+    constexpr bool F8 = DT == DT_FP8;
+    using ET = std::conditional_t<F8, uint8_t, uint16_t>;  // stored element
+    using RT = std::conditional_t<F8, u32x2, u32x4>;       // 8 stored elements
+    static_assert(!F8 || (BIAS && !ROT), "FP8 runs the explicit-score path, without rotary");
     using pf::kLazy;
     __shared__ __attribute__((aligned(16))) uint16_t s_k[2][BN * D];
     __shared__ __attribute__((aligned(16))) uint16_t s_v[2][BN * D];
@@ -240,9 +247,9 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
     const int offsk = kk0 * D + (swzk(kk0, dch) << 3);   // + u*(NT/DCH)*D for chunk u
     const int offsv = kk0 * D + (swzv(kk0, dch) << 3);
 
-    const uint16_t* qp = static_cast<const uint16_t*>(a.q);
-    const uint16_t* kp = static_cast<const uint16_t*>(a.k);
-    const uint16_t* vp = static_cast<const uint16_t*>(a.v);
+    const ET* qp = static_cast<const ET*>(a.q);
+    const ET* kp = static_cast<const ET*>(a.k);
+    const ET* vp = static_cast<const ET*>(a.v);
     uint16_t* op = static_cast<uint16_t*>(a.out);
     const float cs = a.scale_log2;
 
@@ -296,11 +303,17 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
         const int f_lo = key_lo(wi_hi + diag0, a.wl, a.chunk), f_hi = key_hi(wi_lo + diag0, a.wr, a.chunk);
 
         // ---- K/V tiles: registers -> double-buffered LDS ----------------------------------
-        u32x4 kr[CPT], vr[CPT];
+        RT kr[CPT], vr[CPT];
         // per-item row bases: token j of this kv head lives at base + j * si
         // (contiguous / varlen) or at base + blk * sb + (j % page) * si (paged)
-        const uint16_t* kb0 = kp + (int64_t)hk * a.k_sh + dch * 8;
-        const uint16_t* vb0 = vp + (int64_t)hk * a.v_sh + dch * 8;
+        const ET* kb0 = kp + (int64_t)hk * a.k_sh + dch * 8;
+        const ET* vb0 = vp + (int64_t)hk * a.v_sh + dch * 8;
+        // FP8: scores scale by q_descale * k_descale, the output by v_descale
+        float sc_qk = a.scale, sc_v = 1.f;
+        if constexpr (F8) {
+            sc_qk = a.scale * descale_at(a.qd, a.qd_sb, a.qd_sh, b, hk) * descale_at(a.kd, a.kd_sb, a.kd_sh, b, hk);
+            sc_v = descale_at(a.vd, a.vd_sb, a.vd_sh, b, hk);
+        }
         const int* btrow = nullptr;
         if constexpr (PAGED) {
             btrow = a.block_table + (int64_t)crow * a.bt_stride;
@@ -317,8 +330,8 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
             for (int u = 0; u < CPT; ++u) {
                 const int j = t0 + kk0 + u * (NT / DCH);
                 if (j < k_hi && dch * 8 < a.hd) {
-                    const uint16_t* kpr;
-                    const uint16_t* vpr;
+                    const ET* kpr;
+                    const ET* vpr;
                     if constexpr (PAGED) {
                         const int pg = a.page_shift >= 0 ? j >> a.page_shift : j / a.page;
                         const int inp = a.page_shift >= 0 ? j & (a.page - 1) : j % a.page;
@@ -329,19 +342,23 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
                         kpr = kb0 + (int64_t)j * a.k_si;
                         vpr = vb0 + (int64_t)j * a.v_si;
                     }
-                    kr[u] = *reinterpret_cast<const u32x4*>(kpr);
-                    vr[u] = *reinterpret_cast<const u32x4*>(vpr);
+                    kr[u] = *reinterpret_cast<const RT*>(kpr);
+                    vr[u] = *reinterpret_cast<const RT*>(vpr);
                 } else {
-                    kr[u] = u32x4{0u, 0u, 0u, 0u};
-                    vr[u] = u32x4{0u, 0u, 0u, 0u};
+                    kr[u] = RT{};
+                    vr[u] = RT{};
                 }
             }
+        };
+        auto widen = [](RT x) -> u32x4 {
+            if constexpr (F8) return fp8x8_to_bf16(x);
+            else return x;
         };
         auto store_tile = [&](int buf) {
 #pragma unroll
             for (int u = 0; u < CPT; ++u) {
-                *reinterpret_cast<u32x4*>(&s_k[buf][offsk + u * (NT / DCH) * D]) = kr[u];
-                *reinterpret_cast<u32x4*>(&s_v[buf][offsv + u * (NT / DCH) * D]) = vr[u];
+                *reinterpret_cast<u32x4*>(&s_k[buf][offsk + u * (NT / DCH) * D]) = widen(kr[u]);
+                *reinterpret_cast<u32x4*>(&s_v[buf][offsv + u * (NT / DCH) * D]) = widen(vr[u]);
             }
         };
 
@@ -349,7 +366,7 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
         u32x4 qreg[RB][KSTEPS];
         float slope[RB];
         int qi[RB];
-        [[maybe_unused]] const uint16_t* qrows[RB];
+        [[maybe_unused]] const ET* qrows[RB];
         [[maybe_unused]] bool qok[RB];
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
@@ -359,12 +376,12 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
             const int h = hk * g + (ok ? r % g : 0);
             qi[rb] = i;
             slope[rb] = (BIAS && a.alibi && ok) ? a.alibi[(int64_t)b * a.alibi_sb + h] : 0.f;
-            const uint16_t* qrow = a.cu_seqlens_q
-                                       ? qp + ((int64_t)a.cu_seqlens_q[b] + i) * a.q_si + (int64_t)h * a.q_sh
-                                       : qp + (int64_t)b * a.q_sb + (int64_t)i * a.q_si + (int64_t)h * a.q_sh;
+            const ET* qrow = a.cu_seqlens_q
+                                 ? qp + ((int64_t)a.cu_seqlens_q[b] + i) * a.q_si + (int64_t)h * a.q_sh
+                                 : qp + (int64_t)b * a.q_sb + (int64_t)i * a.q_si + (int64_t)h * a.q_sh;
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s)
-                qreg[rb][s] = ok && (G * KSTEPS + s) * 8 < a.hd ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s) * 8)
+                qreg[rb][s] = ok && (G * KSTEPS + s) * 8 < a.hd ? widen(*reinterpret_cast<const RT*>(qrow + (G * KSTEPS + s) * 8))
                                                                 : u32x4{0u, 0u, 0u, 0u};
             qrows[rb] = qrow;
             qok[rb] = ok;
@@ -481,7 +498,7 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
                         float x = sacc[rb][kb][e];
                         const int j = s0 + kb * 16 + G * 4 + e;
                         if constexpr (BIAS) {
-                            float y = x * a.scale;
+                            float y = x * sc_qk;
                             if (a.softcap > 0.f) y = a.softcap * tanhf(y / a.softcap);
                             if (a.alibi) {
                                 int dist = qi[rb] + diag0 - j;
@@ -578,7 +595,7 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
             const int r = wrow0 + rb * 16 + li;
             const float lrow = wave_sum16x4(l_run[rb]);
             const bool nonempty = lrow > 0.f;
-            const float inv = nonempty ? 1.f / lrow : 0.f;
+            const float inv = nonempty ? (F8 ? sc_v / lrow : 1.f / lrow) : 0.f;
             const float lse = nonempty ? (m_run[rb] + fast_log2(lrow)) * kLn2 : (final_out ? INFINITY : -INFINITY);
             if (r < bi.rows) {
                 const int i = r / g, h = hk * g + r % g;
@@ -736,6 +753,9 @@ static void launch_prefill_d(const FwdArgs& a, int dtype, int grid, hipStream_t 
     if (dtype == DT_BF16) {
         if (bias) launch_prefill_b<DT_BF16, HD, true>(a, grid, stream);
         else launch_prefill_b<DT_BF16, HD, false>(a, grid, stream);
+    } else if (dtype == DT_FP8) {
+        // descales of any sign: the explicit-score path; no rotary with FP8
+        launch_prefill_r<DT_FP8, HD, true, false>(a, grid, stream);
     } else {
         if (bias) launch_prefill_b<DT_FP16, HD, true>(a, grid, stream);
         else launch_prefill_b<DT_FP16, HD, false>(a, grid, stream);
@@ -756,7 +776,8 @@ static void launch_merge_d(const FwdArgs& a, int dtype, hipStream_t stream) {
     constexpr int BM = PfCfg<HD>::BM;
     constexpr int RPB = 256 / (HD / 8);
     const int64_t grid = (int64_t)a.B * a.mt_max * a.Hk * ((BM + RPB - 1) / RPB);
-    if (dtype == DT_BF16) hipLaunchKernelGGL((fa_merge_kernel<DT_BF16, HD, BM>), dim3(grid), dim3(256), 0, stream, a);
+    if (dtype == DT_BF16 || dtype == DT_FP8)  // FP8 inputs give a bf16 output
+        hipLaunchKernelGGL((fa_merge_kernel<DT_BF16, HD, BM>), dim3(grid), dim3(256), 0, stream, a);
     else hipLaunchKernelGGL((fa_merge_kernel<DT_FP16, HD, BM>), dim3(grid), dim3(256), 0, stream, a);
 }
 

@@ -74,6 +74,12 @@ struct FwdArgs {
     const int* cu_knew;
     const int* rot_pos;
     int chunk;          // attention_chunk, 0 = off
+    // FP8 inputs: descale factors per (batch, kv head), null = 1; scores are
+    // scaled by qd * kd and the output by vd
+    const float* qd;
+    const float* kd;
+    const float* vd;
+    int64_t qd_sb, qd_sh, kd_sb, kd_sh, vd_sb, vd_sh;
 };
 
 // Backward (dense / varlen). Row layouts as in FwdArgs; lse and dsum share

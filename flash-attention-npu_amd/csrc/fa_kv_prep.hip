@@ -17,28 +17,34 @@
 #include "fa_kernel_args.h"
 #include "fa_rope.h"
 
+#include <type_traits>
+
 namespace fa {
 
 // blockIdx.y: 0 = new keys, 1 = new values, 2 = q rotation. A workgroup
 // covers 256 / U head rows (U = 16-byte chunks per row), one thread per chunk:
 // every thread moves 16 bytes, and all index arithmetic is 32-bit (the host
-// keeps row counts below 2^31).
+// keeps row counts below 2^31). DT_FP8 rows are e4m3fn bytes, copied as they
+// are (the host admits no rotary with FP8).
 template <int DT>
 __global__ void __launch_bounds__(256) fa_kv_prep_kernel(KvPrepArgs a) {
+    constexpr bool F8 = DT == DT_FP8;
+    using ET = std::conditional_t<F8, uint8_t, uint16_t>;
+    constexpr int EPL = 16 / sizeof(ET);  // elements per 16-byte chunk
     const int which = blockIdx.y;
-    const int U = (which == 1 ? a.Dv : a.D) >> 3;
+    const int U = (which == 1 ? a.Dv : a.D) / EPL;
     const int rpb = 256 / U;
     const int tid = threadIdx.x;
     const int rl = tid / U;
     const int u = tid - rl * U;
     if (rl >= rpb) return;
     const int row = blockIdx.x * rpb + rl;
-    const int rd = which == 1 ? 0 : a.rotary_dim;
+    const int rd = (which == 1 || F8) ? 0 : a.rotary_dim;
     const uint16_t* cs = static_cast<const uint16_t*>(a.cos);
     const uint16_t* sn = static_cast<const uint16_t*>(a.sin);
 
-    const uint16_t* src;
-    uint16_t* dst;
+    const ET* src;
+    ET* dst;
     int pos;
     if (which == 2) {
         const int h = row % a.H;
@@ -48,14 +54,14 @@ __global__ void __launch_bounds__(256) fa_kv_prep_kernel(KvPrepArgs a) {
             if (row >= a.total_q * a.H) return;
             b = seq_of(a.cu_q, a.B, bi);
             i = bi - a.cu_q[b];
-            src = static_cast<const uint16_t*>(a.q) + (int64_t)bi * a.q_si + (int64_t)h * a.q_sh;
+            src = static_cast<const ET*>(a.q) + (int64_t)bi * a.q_si + (int64_t)h * a.q_sh;
         } else {
             if (row >= a.B * a.Sq * a.H) return;
             i = bi % a.Sq;
             b = bi / a.Sq;
-            src = static_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_sb + (int64_t)i * a.q_si + (int64_t)h * a.q_sh;
+            src = static_cast<const ET*>(a.q) + (int64_t)b * a.q_sb + (int64_t)i * a.q_si + (int64_t)h * a.q_sh;
         }
-        dst = static_cast<uint16_t*>(a.q_out) + (int64_t)row * a.D;
+        dst = static_cast<ET*>(a.q_out) + (int64_t)row * a.D;
         pos = (a.rot_pos ? a.rot_pos[b] : a.seqlens ? a.seqlens[b] : 0) + (a.q_same_pos ? 0 : i);
     } else {
         const int h = row % a.Hk;
@@ -76,7 +82,7 @@ __global__ void __launch_bounds__(256) fa_kv_prep_kernel(KvPrepArgs a) {
         const int j = a.seqlens[b] + t;
         if (j < 0 || j >= a.kv_capacity) return;  // cache too small: nothing is written
         const int crow = a.batch_idx ? a.batch_idx[b] : b;
-        uint16_t* cache = static_cast<uint16_t*>(which == 0 ? a.k_cache : a.v_cache);
+        ET* cache = static_cast<ET*>(which == 0 ? a.k_cache : a.v_cache);
         const int64_t sb = which == 0 ? a.k_sb : a.v_sb, si = which == 0 ? a.k_si : a.v_si,
                       sh = which == 0 ? a.k_sh : a.v_sh;
         if (a.block_table) {
@@ -88,30 +94,34 @@ __global__ void __launch_bounds__(256) fa_kv_prep_kernel(KvPrepArgs a) {
             if (crow < 0 || crow >= a.batch_cache) return;
             dst = cache + (int64_t)crow * sb + (int64_t)j * si + (int64_t)h * sh;
         }
-        src = which == 0 ? static_cast<const uint16_t*>(a.k_new) + src_off + (int64_t)h * a.kn_sh
-                         : static_cast<const uint16_t*>(a.v_new) + src_off + (int64_t)h * a.vn_sh;
+        src = which == 0 ? static_cast<const ET*>(a.k_new) + src_off + (int64_t)h * a.kn_sh
+                         : static_cast<const ET*>(a.v_new) + src_off + (int64_t)h * a.vn_sh;
         pos = a.rot_pos ? a.rot_pos[b] + t : j;
     }
-    u32x4 x = *reinterpret_cast<const u32x4*>(src + 8 * u);
-    if (8 * u < rd) {
-        pos = min(max(pos, 0), a.seqlen_ro - 1);
-        x = rope_chunk<DT>(x, src, u, rd, a.interleaved != 0, cs + (int64_t)pos * a.cs_stride,
-                           sn + (int64_t)pos * a.cs_stride);
+    u32x4 x = *reinterpret_cast<const u32x4*>(src + EPL * u);
+    if constexpr (!F8) {
+        if (8 * u < rd) {
+            pos = min(max(pos, 0), a.seqlen_ro - 1);
+            x = rope_chunk<DT>(x, src, u, rd, a.interleaved != 0, cs + (int64_t)pos * a.cs_stride,
+                               sn + (int64_t)pos * a.cs_stride);
+        }
     }
-    *reinterpret_cast<u32x4*>(dst + 8 * u) = x;
+    *reinterpret_cast<u32x4*>(dst + EPL * u) = x;
 }
 
 hipError_t launch_kv_prep(const KvPrepArgs& a, int dtype, hipStream_t stream) {
     const int64_t rows_kv = !a.k_new ? 0 : a.cu_knew ? (int64_t)a.total_new * a.Hk : (int64_t)a.B * a.S_new * a.Hk;
     const int64_t rows_q = !a.q_out ? 0 : a.cu_q ? (int64_t)a.total_q * a.H : (int64_t)a.B * a.Sq * a.H;
     if (rows_kv >= INT32_MAX || rows_q >= INT32_MAX) return hipErrorInvalidValue;
-    const int rpb = 256 / ((a.D > a.Dv ? a.D : a.Dv) >> 3);
+    const int rpb = 256 / ((a.D > a.Dv ? a.D : a.Dv) / (dtype == DT_FP8 ? 16 : 8));
     const int64_t mx = rows_kv > rows_q ? rows_kv : rows_q;
     if (mx == 0) return hipSuccess;
     const int grid = (int)((mx + rpb - 1) / rpb);
     const int ny = a.q_out ? 3 : 2;
     if (dtype == DT_BF16)
         hipLaunchKernelGGL(fa_kv_prep_kernel<DT_BF16>, dim3(grid, ny), dim3(256), 0, stream, a);
+    else if (dtype == DT_FP8)
+        hipLaunchKernelGGL(fa_kv_prep_kernel<DT_FP8>, dim3(grid, ny), dim3(256), 0, stream, a);
     else
         hipLaunchKernelGGL(fa_kv_prep_kernel<DT_FP16>, dim3(grid, ny), dim3(256), 0, stream, a);
     return hipGetLastError();

@@ -29,7 +29,13 @@ using OptT = std::optional<Tensor>;
 int32_t dtype_code(const Tensor& t) {
     if (t.scalar_type() == at::kHalf) return FA_DTYPE_FP16;
     if (t.scalar_type() == at::kBFloat16) return FA_DTYPE_BF16;
+    if (t.scalar_type() == at::kFloat8_e4m3fn) return FA_DTYPE_FP8_E4M3;
     TORCH_CHECK(false, "FlashAttention only support fp16 and bf16 data type");
+}
+
+// out has q's shape; FP8 (e4m3) inputs give a bf16 out, as in Dao's v3 API
+at::TensorOptions out_options(const Tensor& q) {
+    return q.scalar_type() == at::kFloat8_e4m3fn ? q.options().dtype(at::kBFloat16) : q.options();
 }
 
 void check_status(fa_status_t st) { TORCH_CHECK(st == FA_OK, "fa_mi355x: ", fa_last_error()); }
@@ -61,6 +67,24 @@ void set_window(fa_fwd_params& p, bool is_causal, int64_t wl, int64_t wr) {
     p.window_size_right = (int32_t)wr;
 }
 
+// q_descale / k_descale / v_descale: fp32 (batch_size, num_heads_k), read for FP8 inputs only
+// (their shape per csrc/arch22/flash_attn_npu_v3/flash_api.cpp:82-84 of the reference)
+void set_descale(fa_fwd_params& p, const OptT& qd, const OptT& kd, const OptT& vd, const Tensor& q, int64_t batch) {
+    auto one = [&](const OptT& t, const char* name, const float*& ptr, int64_t& sb, int64_t& sh) {
+        if (!t.has_value()) return;
+        check_dev(*t, q, name);
+        TORCH_CHECK(t->scalar_type() == at::kFloat, name, " must have dtype fp32");
+        TORCH_CHECK(t->dim() == 2 && t->size(0) == batch && t->size(1) == p.nheads_k, name,
+                    " must have shape (batch_size, num_heads_k)");
+        ptr = t->data_ptr<float>();
+        sb = t->stride(0);
+        sh = t->stride(1);
+    };
+    one(qd, "q_descale", p.q_descale, p.q_descale_batch_stride, p.q_descale_head_stride);
+    one(kd, "k_descale", p.k_descale, p.k_descale_batch_stride, p.k_descale_head_stride);
+    one(vd, "v_descale", p.v_descale, p.v_descale_batch_stride, p.v_descale_head_stride);
+}
+
 void set_alibi(fa_fwd_params& p, const OptT& alibi, const Tensor& q, int64_t batch, int64_t nheads) {
     if (!alibi.has_value()) return;
     check_dev(*alibi, q, "alibi_slopes");
@@ -84,7 +108,8 @@ std::tuple<Tensor, Tensor> kvcache_impl(const Tensor& q, Tensor& kcache, Tensor&
                                         const OptT& cu_seqlens_k_new, int64_t max_seqlen_q,
                                         const OptT& rotary_seqlens, double softmax_scale, bool is_causal,
                                         int64_t window_size_left, int64_t window_size_right, int64_t attention_chunk,
-                                        double softcap, bool is_rotary_interleaved, int64_t num_splits) {
+                                        double softcap, bool is_rotary_interleaved, int64_t num_splits,
+                                        const OptT& q_descale, const OptT& k_descale, const OptT& v_descale) {
     c10::DeviceGuard guard(q.device());
     TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
     check_dev(kcache, q, "k_cache");
@@ -219,7 +244,8 @@ std::tuple<Tensor, Tensor> kvcache_impl(const Tensor& q, Tensor& kcache, Tensor&
     set_window(p, is_causal, window_size_left, window_size_right);
     p.attention_chunk = (int32_t)attention_chunk;
     p.num_splits = (int32_t)num_splits;
-    Tensor out = at::empty(q.sizes(), q.options());
+    set_descale(p, q_descale, k_descale, v_descale, q, batch);
+    Tensor out = at::empty(q.sizes(), out_options(q));
     Tensor lse = ragged_q ? at::empty({q.size(1), q.size(0)}, q.options().dtype(at::kFloat))
                           : at::empty({q.size(0), q.size(2), q.size(1)}, q.options().dtype(at::kFloat));
     p.out = out.data_ptr();
@@ -249,7 +275,7 @@ std::tuple<Tensor, Tensor> fwd_kvcache(const Tensor& q, Tensor& kcache, Tensor& 
     return kvcache_impl(q, kcache, vcache, k_new, v_new, seqlens_k, rotary_cos, rotary_sin, cache_batch_idx,
                         leftpad_k, block_table, alibi_slopes, std::nullopt, std::nullopt, 0, std::nullopt,
                         softmax_scale, is_causal, window_size_left, window_size_right, 0, softcap,
-                        is_rotary_interleaved, num_splits);
+                        is_rotary_interleaved, num_splits, std::nullopt, std::nullopt, std::nullopt);
 }
 
 std::tuple<Tensor, Tensor> fwd_kvcache_v3(const Tensor& q, Tensor& kcache, Tensor& vcache, const OptT& k_new,
@@ -261,17 +287,20 @@ std::tuple<Tensor, Tensor> fwd_kvcache_v3(const Tensor& q, Tensor& kcache, Tenso
                                           const OptT& rotary_seqlens, double softmax_scale, bool is_causal,
                                           int64_t window_size_left, int64_t window_size_right,
                                           int64_t attention_chunk, double softcap, bool is_rotary_interleaved,
-                                          int64_t num_splits) {
+                                          int64_t num_splits, const OptT& q_descale, const OptT& k_descale,
+                                          const OptT& v_descale) {
     return kvcache_impl(q, kcache, vcache, k_new, v_new, seqlens_k, rotary_cos, rotary_sin, cache_batch_idx,
                         leftpad_k, block_table, alibi_slopes, cu_seqlens_q, cu_seqlens_k_new, max_seqlen_q,
                         rotary_seqlens, softmax_scale, is_causal, window_size_left, window_size_right,
-                        attention_chunk, softcap, is_rotary_interleaved, num_splits);
+                        attention_chunk, softcap, is_rotary_interleaved, num_splits, q_descale, k_descale,
+                        v_descale);
 }
 
 // ---- flash_attn_func ------------------------------------------------------------------------
 std::tuple<Tensor, Tensor> fwd(const Tensor& q, const Tensor& k, const Tensor& v, const OptT& alibi_slopes,
                                double p_dropout, double softmax_scale, bool is_causal, int64_t window_size_left,
-                               int64_t window_size_right, double softcap, int64_t attention_chunk) {
+                               int64_t window_size_right, double softcap, int64_t attention_chunk,
+                               const OptT& q_descale, const OptT& k_descale, const OptT& v_descale) {
     c10::DeviceGuard guard(q.device());
     TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
     check_dev(k, q, "k");
@@ -314,7 +343,8 @@ std::tuple<Tensor, Tensor> fwd(const Tensor& q, const Tensor& k, const Tensor& v
     set_window(p, is_causal, window_size_left, window_size_right);
     p.attention_chunk = (int32_t)attention_chunk;
     p.num_splits = 0;
-    Tensor out = at::empty(q.sizes(), q.options());
+    set_descale(p, q_descale, k_descale, v_descale, q, q.size(0));
+    Tensor out = at::empty(q.sizes(), out_options(q));
     Tensor lse = at::empty({q.size(0), q.size(2), q.size(1)}, q.options().dtype(at::kFloat));
     p.out = out.data_ptr();
     p.out_batch_stride = out.stride(0);
@@ -334,7 +364,8 @@ std::tuple<Tensor, Tensor> varlen_fwd(const Tensor& q, const Tensor& k, const Te
                                       const OptT& alibi_slopes,
                                       int64_t max_seqlen_q, int64_t max_seqlen_k, double p_dropout,
                                       double softmax_scale, bool is_causal, int64_t window_size_left,
-                                      int64_t window_size_right, double softcap, int64_t attention_chunk) {
+                                      int64_t window_size_right, double softcap, int64_t attention_chunk,
+                                      const OptT& q_descale, const OptT& k_descale, const OptT& v_descale) {
     c10::DeviceGuard guard(q.device());
     TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
     check_dev(k, q, "k");
@@ -402,7 +433,8 @@ std::tuple<Tensor, Tensor> varlen_fwd(const Tensor& q, const Tensor& k, const Te
     set_window(p, is_causal, window_size_left, window_size_right);
     p.attention_chunk = (int32_t)attention_chunk;
     p.num_splits = 0;
-    Tensor out = at::empty(q.sizes(), q.options());
+    set_descale(p, q_descale, k_descale, v_descale, q, p.batch);
+    Tensor out = at::empty(q.sizes(), out_options(q));
     Tensor lse = at::empty({q.size(1), q.size(0)}, q.options().dtype(at::kFloat));
     p.out = out.data_ptr();
     p.out_batch_stride = 0;
@@ -622,19 +654,21 @@ TORCH_LIBRARY(fa_mi355x, m) {
         "float softcap, bool is_rotary_interleaved, int num_splits) -> (Tensor, Tensor)");
     m.def(
         "fwd(Tensor q, Tensor k, Tensor v, Tensor? alibi_slopes, float p_dropout, float softmax_scale, bool is_causal, "
-        "int window_size_left, int window_size_right, float softcap, int attention_chunk=0) -> (Tensor, Tensor)");
+        "int window_size_left, int window_size_right, float softcap, int attention_chunk=0, Tensor? q_descale=None, "
+        "Tensor? k_descale=None, Tensor? v_descale=None) -> (Tensor, Tensor)");
     m.def(
         "fwd_kvcache_v3(Tensor q, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor? k, Tensor? v, Tensor? seqlens_k, "
         "Tensor? rotary_cos, Tensor? rotary_sin, Tensor? cache_batch_idx, Tensor? leftpad_k, Tensor? block_table, "
         "Tensor? alibi_slopes, Tensor? cu_seqlens_q, Tensor? cu_seqlens_k_new, int max_seqlen_q, "
         "Tensor? rotary_seqlens, float softmax_scale, bool is_causal, int window_size_left, int window_size_right, "
-        "int attention_chunk, float softcap, bool is_rotary_interleaved, int num_splits) -> (Tensor, Tensor)");
+        "int attention_chunk, float softcap, bool is_rotary_interleaved, int num_splits, Tensor? q_descale=None, "
+        "Tensor? k_descale=None, Tensor? v_descale=None) -> (Tensor, Tensor)");
     m.def(
         "varlen_fwd(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor? cu_seqlens_k, Tensor? seqused_k, "
         "Tensor? block_table, "
         "Tensor? alibi_slopes, int max_seqlen_q, int max_seqlen_k, float p_dropout, float softmax_scale, "
-        "bool is_causal, int window_size_left, int window_size_right, float softcap, int attention_chunk=0) "
-        "-> (Tensor, Tensor)");
+        "bool is_causal, int window_size_left, int window_size_right, float softcap, int attention_chunk=0, "
+        "Tensor? q_descale=None, Tensor? k_descale=None, Tensor? v_descale=None) -> (Tensor, Tensor)");
     m.def("fwd_combine(Tensor out_partial, Tensor lse_partial, Tensor? out, ScalarType? out_dtype) -> (Tensor, Tensor)");
     m.def(
         "bwd(Tensor dout, Tensor q, Tensor k, Tensor v, Tensor out, Tensor softmax_lse, Tensor? alibi_slopes, "

@@ -11,9 +11,9 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 CORE_LIB = os.path.join(_HERE, "lib", "libfa_mi355x.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 FA_OK, FA_EINVAL, FA_EUNSUPPORTED, FA_EHIP, FA_EWORKSPACE = 0, 1, 2, 3, 4
-FA_DTYPE_FP16, FA_DTYPE_BF16, FA_DTYPE_FP32 = 0, 1, 2
+FA_DTYPE_FP16, FA_DTYPE_BF16, FA_DTYPE_FP32, FA_DTYPE_FP8_E4M3 = 0, 1, 2, 3
 FA_KIND_KVCACHE, FA_KIND_DENSE, FA_KIND_VARLEN = 0, 1, 2
 
 EXPORTED = ["fa_abi_version", "fa_validate", "fa_fwd_workspace_size", "fa_mha_fwd_kvcache", "fa_mha_fwd",
@@ -50,6 +50,9 @@ class FwdParams(ctypes.Structure):
         ("stage_events", _vp),
         ("cache_leftpad", _vp), ("cu_seqlens_k_new", _vp), ("total_k_new", _i32), ("rotary_seqlens", _vp),
         ("attention_chunk", _i32),
+        ("q_descale", _vp), ("q_descale_batch_stride", _i64), ("q_descale_head_stride", _i64),
+        ("k_descale", _vp), ("k_descale_batch_stride", _i64), ("k_descale_head_stride", _i64),
+        ("v_descale", _vp), ("v_descale_batch_stride", _i64), ("v_descale_head_stride", _i64),
     ]
 
 

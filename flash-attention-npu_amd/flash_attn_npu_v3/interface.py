@@ -8,6 +8,13 @@ The reference routes all three through one custom op (:63-154); here each
 maps onto the matching fa_mi355x operator. flash_attn_func and
 flash_attn_varlen_func have a backward (the reference's :536-698 autograd
 Functions), run by the MI355X backward kernels.
+
+FP8: q, k, v (and the cache, k / v of flash_attn_with_kvcache) may be
+torch.float8_e4m3fn with q_descale / k_descale / v_descale of shape
+(batch_size, nheads_k) fp32; scores are scaled by q_descale * k_descale and
+the output by v_descale, and out is bf16 (forward only, no rotary). The
+reference rejects the descales (csrc/arch22/flash_attn_npu_v3/
+flash_api.cpp:154-156).
 """
 from typing import Optional, Union
 
@@ -49,13 +56,14 @@ class FlashAttnFunc(torch.autograd.Function):
     def forward(ctx, q, k, v, softmax_scale, causal, qv=None, q_descale=None, k_descale=None, v_descale=None,
                 window_size=(-1, -1), attention_chunk=0, softcap=0.0, num_splits=1, pack_gqa=None,
                 deterministic=False, sm_margin=0, return_softmax=False, scheduler_metadata=None):
-        _reject(qv=qv, q_descale=q_descale, k_descale=k_descale, v_descale=v_descale)
+        _reject(qv=qv)
         if softmax_scale is None:
             softmax_scale = q.shape[-1] ** (-0.5)
         _check_metadata(scheduler_metadata, q.device)
         q, k, v = [maybe_contiguous(x) for x in (q, k, v)]
         out, softmax_lse = ops.fwd(q, k, v, None, 0.0, float(softmax_scale), bool(causal), int(window_size[0]),
-                                   int(window_size[1]), float(softcap), int(attention_chunk))
+                                   int(window_size[1]), float(softcap), int(attention_chunk), q_descale, k_descale,
+                                   v_descale)
         if any(x.requires_grad for x in (q, k, v)):
             ctx.save_for_backward(q, k, v, out, softmax_lse)
             ctx.softmax_scale = softmax_scale
@@ -82,7 +90,7 @@ class FlashAttnVarlenFunc(torch.autograd.Function):
                 softmax_scale, causal, qv=None, q_descale=None, k_descale=None, v_descale=None, window_size=(-1, -1),
                 attention_chunk=0, softcap=0.0, num_splits=1, pack_gqa=None, deterministic=False, sm_margin=0,
                 return_softmax=False, scheduler_metadata=None):
-        _reject(seqused_q=seqused_q, qv=qv, q_descale=q_descale, k_descale=k_descale, v_descale=v_descale)
+        _reject(seqused_q=seqused_q, qv=qv)
         if softmax_scale is None:
             softmax_scale = q.shape[-1] ** (-0.5)
         _check_metadata(scheduler_metadata, q.device)
@@ -90,7 +98,7 @@ class FlashAttnVarlenFunc(torch.autograd.Function):
         out, softmax_lse = ops.varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, None, None,
                                           int(max_seqlen_q), int(max_seqlen_k), 0.0, float(softmax_scale),
                                           bool(causal), int(window_size[0]), int(window_size[1]), float(softcap),
-                                          int(attention_chunk))
+                                          int(attention_chunk), q_descale, k_descale, v_descale)
         if any(x.requires_grad for x in (q, k, v)):
             ctx.save_for_backward(q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k)
             ctx.has_seqused_k = seqused_k is not None
@@ -170,12 +178,14 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None, rotary
     by cu_seqlens_k_new. cache_leftpad[b] is the first valid cache row of
     sequence b (contiguous caches). Rotary positions start at rotary_seqlens[b]
     (default cache_seqlens[b]). attention_chunk > 0 restricts each query to
-    the keys of its own chunk of that size. Returns out, or (out, softmax_lse,
+    the keys of its own chunk of that size. With float8_e4m3fn q / caches / k / v,
+    q_descale, k_descale and v_descale ((batch_size, nheads_k) fp32) scale the
+    scores and the output, and out is bf16. Returns out, or (out, softmax_lse,
     out_accum, lse_accum) when return_softmax_lse (the accumulators are empty
     tensors)."""
     assert k_cache.stride(-1) == 1, "k_cache must have contiguous last dimension"
     assert v_cache.stride(-1) == 1, "v_cache must have contiguous last dimension"
-    _reject(qv=qv, q_descale=q_descale, k_descale=k_descale, v_descale=v_descale)
+    _reject(qv=qv)
     if softmax_scale is None:
         softmax_scale = q.shape[-1] ** (-0.5)
     batch = q.shape[0] if cu_seqlens_q is None else cu_seqlens_q.numel() - 1
@@ -198,7 +208,7 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None, rotary
         out, softmax_lse = ops.varlen_fwd(q, k_cache, v_cache, cu_seqlens_q, cu_k, cache_seqlens, None, None,
                                           int(max_seqlen_q), int(k_cache.shape[0]), 0.0, float(softmax_scale),
                                           bool(causal), int(window_size[0]), int(window_size[1]), float(softcap),
-                                          int(attention_chunk))
+                                          int(attention_chunk), q_descale, k_descale, v_descale)
     else:
         # (batch, seqlen) or ragged (total_q) queries against a (batch_cache,
         # seqlen_cache) or paged cache, with the in-place append of k / v
@@ -210,7 +220,8 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None, rotary
                                               int(max_seqlen_q or 0), maybe_contiguous(rotary_seqlens),
                                               float(softmax_scale), bool(causal), int(window_size[0]),
                                               int(window_size[1]), int(attention_chunk), float(softcap),
-                                              bool(rotary_interleaved), int(num_splits))
+                                              bool(rotary_interleaved), int(num_splits), q_descale, k_descale,
+                                              v_descale)
     if return_softmax_lse:
         oa, la = _empty_accum(out)
         return out, softmax_lse, oa, la

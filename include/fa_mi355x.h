@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define FA_MI355X_ABI_VERSION 2
+#define FA_MI355X_ABI_VERSION 3
 
 typedef enum {
     FA_OK = 0,
@@ -55,7 +55,13 @@ typedef enum {
     FA_EWORKSPACE = 4     /* workspace missing or too small */
 } fa_status_t;
 
-typedef enum { FA_DTYPE_FP16 = 0, FA_DTYPE_BF16 = 1, FA_DTYPE_FP32 = 2 /* fa_combine output only */ } fa_dtype_t;
+typedef enum {
+    FA_DTYPE_FP16 = 0,
+    FA_DTYPE_BF16 = 1,
+    FA_DTYPE_FP32 = 2,     /* fa_combine output only */
+    FA_DTYPE_FP8_E4M3 = 3  /* forward only: q, k, v, k_new, v_new in OCP float8 e4m3fn (torch.float8_e4m3fn),
+                              out in bf16; see q_descale below */
+} fa_dtype_t;
 
 typedef enum {
     FA_KIND_KVCACHE = 0,  /* flash_attn_with_kvcache */
@@ -65,7 +71,8 @@ typedef enum {
 
 typedef struct fa_fwd_params {
     int32_t abi_version;  /* FA_MI355X_ABI_VERSION */
-    int32_t dtype;        /* fa_dtype_t, shared by q, k, v, k_new, v_new, out, rotary cos/sin */
+    int32_t dtype;        /* fa_dtype_t, shared by q, k, v, k_new, v_new, out, rotary cos/sin
+                             (FP8_E4M3: out is bf16, no rotary) */
 
     int32_t batch;        /* B (query batch) */
     int32_t seqlen_q;     /* Sq (dense/kvcache), max_seqlen_q (varlen) */
@@ -149,6 +156,25 @@ typedef struct fa_fwd_params {
     int32_t attention_chunk;         /* > 0: a query sees only keys of its own chunk
                                         [c*floor(p/c), c*floor(p/c) + c) of its diagonal position p,
                                         intersected with the causal / local window */
+
+    /* ---- FP8 inputs (dtype FA_DTYPE_FP8_E4M3; ABI 3) ----
+       Descale factors of the v3 API (q_descale / k_descale / v_descale of
+       flash_attn_func, flash_attn_varlen_func and flash_attn_with_kvcache,
+       flash_attn_npu_v3/interface_arch22.py:797-965; the reference declares them
+       (b, h_k) at csrc/arch22/flash_attn_npu_v3/flash_api.cpp:82-84 and rejects
+       them at :154-156): fp32, shape (B, Hk),
+       strides in elements; NULL = 1. With x8 the stored e4m3 values, sequence b
+       and kv head hk = h / (H / Hk):
+         scores = softmax_scale * q_descale[b,hk] * k_descale[b,hk] * (q8 . k8)
+         out    = v_descale[b,hk] * softmax(scores) . v8
+       The softmax_lse is that of these scores. headdim must be a multiple of
+       16; rotary and the backward are not available for FP8. */
+    const float* q_descale;
+    int64_t q_descale_batch_stride, q_descale_head_stride;
+    const float* k_descale;
+    int64_t k_descale_batch_stride, k_descale_head_stride;
+    const float* v_descale;
+    int64_t v_descale_batch_stride, v_descale_head_stride;
 } fa_fwd_params;
 
 /* Library / ABI version. */

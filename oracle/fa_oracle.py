@@ -237,6 +237,59 @@ def attention(q, k, v, *, dtype, scale, softcap=0.0, causal=False, window=(-1, -
     return out, lse
 
 
+def e4m3_to_bf16_bits(x8):
+    """OCP 8-bit floating point E4M3 ("e4m3fn": torch.float8_e4m3fn) bytes ->
+    bf16 bit patterns. Definition (OCP 8-bit Floating Point Specification
+    v1.0, E4M3): sign bit, 4-bit exponent with bias 7, 3-bit mantissa;
+    exponent 0 is subnormal (m/8 * 2^-6); S.1111.111 is NaN; no infinities.
+    Every E4M3 value has at most 4 significant bits, so the bf16 pattern is
+    the exact value. Used for the FP8 inputs of the v3 API (q_descale /
+    k_descale / v_descale, flash_attn_npu_v3/interface_arch22.py:797-965 of
+    the reference, which rejects them at csrc/arch22/flash_attn_npu_v3/
+    flash_api.cpp:154-156)."""
+    x = np.asarray(x8, dtype=np.uint8).astype(np.int32)
+    s = (x >> 7) & 1
+    e = (x >> 3) & 15
+    m = x & 7
+    val = np.where(e > 0, np.ldexp(1.0 + m / 8.0, e - 7), np.ldexp(m / 8.0, -6))
+    val = np.where(s == 1, -val, val).astype(np.float32)
+    val = np.where((e == 15) & (m == 7), np.float32(np.nan), val)
+    return (val.view(np.uint32) >> 16).astype(np.uint16)
+
+
+def attention_fp8(q8, k8, v8, *, scale, q_descale=None, k_descale=None, v_descale=None, causal=False,
+                  window=(-1, -1), softcap=0.0, seqlens_k=None, nthreads=1):
+    """FP8 forward on (B, S, H, D) q and (B, Sk, Hk, D) k / v e4m3 bytes
+    (dense, or a contiguous cache with seqlens_k): the values widen exactly
+    to bf16 and, for sequence b and kv head hk, the scores use
+    scale * q_descale[b, hk] * k_descale[b, hk] and the output is multiplied
+    by v_descale[b, hk] (descales (B, Hk) fp32, None = 1). Runs the blockwise
+    golden per (b, hk) with that scale and bf16 arithmetic.
+    Returns (out float32 like q, lse float32 (B, H, Sq))."""
+    q = e4m3_to_bf16_bits(q8)
+    k = e4m3_to_bf16_bits(k8)
+    v = e4m3_to_bf16_bits(v8)
+    B, Sq, H, D = q.shape
+    Hk = k.shape[2]
+    g = H // Hk
+    one = np.ones((B, Hk), dtype=np.float32)
+    qd = one if q_descale is None else np.asarray(q_descale, dtype=np.float32)
+    kd = one if k_descale is None else np.asarray(k_descale, dtype=np.float32)
+    vd = one if v_descale is None else np.asarray(v_descale, dtype=np.float32)
+    out = np.zeros((B, Sq, H, v.shape[3]), dtype=np.float32)
+    lse = np.zeros((B, H, Sq), dtype=np.float32)
+    for b in range(B):
+        for hk in range(Hk):
+            sc = float(np.float32(scale) * qd[b, hk] * kd[b, hk])
+            o, l = attention(q[b:b + 1, :, hk * g:(hk + 1) * g], k[b:b + 1, :, hk:hk + 1], v[b:b + 1, :, hk:hk + 1],
+                             dtype=BF16, scale=sc, softcap=softcap, causal=causal, window=window,
+                             seqlens_k=None if seqlens_k is None else np.asarray(seqlens_k)[b:b + 1],
+                             nthreads=nthreads)
+            out[b, :, hk * g:(hk + 1) * g] = from_bits(o, BF16)[0] * vd[b, hk]
+            lse[b, hk * g:(hk + 1) * g] = l[0]
+    return out, lse
+
+
 def rotary(x, cos, sin, seqlens, *, dtype, interleaved, same_pos=False):
     """Rotary on (B, S, H, D) bits at positions seqlens[b] + i (or seqlens[b])."""
     x = np.array(x, dtype=np.uint16, copy=True, order="C")

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(capi):
     for n in names:
         assert hasattr(lib, n), f"libfa_mi355x.so does not export {n}"
     assert sorted(capi.EXPORTED) == names
-    assert capi.lib().fa_abi_version() == capi.ABI_VERSION == 2
+    assert capi.lib().fa_abi_version() == capi.ABI_VERSION == 3
 
 
 @pytest.mark.parametrize("struct", ["fa_fwd_params", "fa_bwd_params"])
@@ -91,6 +91,7 @@ def test_validate_bwd(capi):
         (dict(attention_chunk=-1), capi.FA_KIND_DENSE, capi.FA_EINVAL, "attention_chunk"),
         (dict(), capi.FA_KIND_VARLEN, capi.FA_EINVAL, "cu_seqlens_q and cu_seqlens_k are required"),
         (dict(), capi.FA_KIND_KVCACHE, capi.FA_EINVAL, "dense or varlen"),
+        (dict(dtype=capi.FA_DTYPE_FP8_E4M3), capi.FA_KIND_DENSE, capi.FA_EINVAL, "only support fp16 and bf16"),
     ]
     for kw, kind, code, msg in bad:
         assert capi.validate_bwd(_valid_bwd(capi, **kw), kind) == code, kw
@@ -123,6 +124,11 @@ def test_validate_accepts_a_valid_call(capi):
                                 vnew_head_stride=128, cu_seqlens_q=0xF0000, total_q=7, cache_leftpad=0xD0000,
                                 attention_chunk=64), capi.FA_KIND_KVCACHE) == capi.FA_OK
     assert capi.validate(_valid(capi, attention_chunk=128), capi.FA_KIND_DENSE) == capi.FA_OK
+    # FP8 (e4m3) inputs with per (batch, kv head) descales; headdim a multiple of 16
+    for d in (64, 96, 128, 192, 256):
+        assert capi.validate(_valid(capi, dtype=capi.FA_DTYPE_FP8_E4M3, headdim=d, headdim_v=d,
+                                    q_descale=0x11000, q_descale_batch_stride=2, q_descale_head_stride=1,
+                                    k_descale=0x12000, v_descale=0x13000), capi.FA_KIND_DENSE) == capi.FA_OK, d
 
 
 BAD = [
@@ -153,6 +159,13 @@ BAD = [
     (dict(cu_seqlens_k_new=0xE0000, total_k_new=3), 0, "EINVAL", "without new keys"),
     (dict(cache_leftpad=0xD0000), 1, "EINVAL", "only valid for the kvcache forward"),
     (dict(cu_seqlens_q=0xF0000, total_q=-1), 0, "EINVAL", "total_q must be >= 0"),
+    (dict(dtype=3, headdim=72, headdim_v=72), 1, "EINVAL", "multiple of 16"),
+    (dict(dtype=3, k_row_stride=264), 0, "EINVAL", "FP8 q, k and v strides"),
+    (dict(dtype=3, k_new=0x70000, v_new=0x80000, seqlen_new=1, knew_batch_stride=256, knew_row_stride=256,
+          knew_head_stride=128, vnew_batch_stride=256, vnew_row_stride=256, vnew_head_stride=128,
+          rotary_cos=0x90000, rotary_sin=0xA0000, rotary_dim=64, seqlen_ro=16), 0, "EINVAL",
+     "rotary is not supported with FP8"),
+    (dict(dtype=4), 1, "EINVAL", "only support fp16 and bf16"),
 ]
 
 
