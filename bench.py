@@ -17,10 +17,11 @@ gets W untimed warmup calls, then untimed calls for about 150 ms more (the
 shader clock ramps up after the idle gap spent building the config's inputs),
 then exactly K timed calls.
 
-`configs` also carries "bwd", the backward of a dense causal training shape
-(not a BASELINE config).
+`configs` also carries "bwd", the backward of a dense causal training shape,
+and "c2f8" / "c3f8", configs 2 and 3 with q, the caches and the new k/v in
+float8_e4m3fn (bf16 out); none of these is a BASELINE config.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c3,c4,c5,bwd] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c3,c4,c5,bwd,c2f8,c3f8] [--no-cpu]
 """
 import argparse
 import ctypes
@@ -78,12 +79,17 @@ def build_case(name, torch, dev, ncopy):
     D = 128
     keep = []
 
+    # "c2f8" / "c3f8": the same workloads with q, the caches and k/v in
+    # float8_e4m3fn (N(0,1) values rounded to e4m3, unit descales), out bf16
+    f8 = name.endswith("f8")
+    base = name[:-2] if f8 else name
+
     def rn(*shape):
-        t = torch.randn(shape, generator=g, device=dev, dtype=torch.float32).to(bf)
-        return t
+        t = torch.randn(shape, generator=g, device=dev, dtype=torch.float32)
+        return t.to(torch.float8_e4m3fn) if f8 else t.to(bf)
 
     c = {"name": name}
-    if name == "c2":
+    if base == "c2":
         g.manual_seed(2); gc.manual_seed(2)
         B, Sq, H, Hk, cap = 32, 1, 32, 8, 8192
         L = torch.randint(1024, 8192, (B,), generator=gc, dtype=torch.int32)
@@ -95,7 +101,7 @@ def build_case(name, torch, dev, ncopy):
         s_new = 1
         kv_tokens = int((L + 1).sum())
         c["work_desc"] = "B32 Sq1 H32/8 D128 bf16 contiguous cache 32x8192, L~U[1024,8191], 1-token append"
-    elif name == "c3":
+    elif base == "c3":
         g.manual_seed(3); gc.manual_seed(3)
         B, Sq, H, Hk, page = 64, 1, 64, 8, 256
         L = torch.round(torch.exp(torch.empty(B).uniform_(math.log(512), math.log(32768), generator=gc))).to(torch.int32)
@@ -118,7 +124,7 @@ def build_case(name, torch, dev, ncopy):
         kv_tokens = int((L + 1).sum())
         cap = maxb * page
         c["work_desc"] = "B64 Sq1 H64/8 D128 bf16 paged(256) permuted block_table, L log-uniform [512,32768], 1-token append"
-    elif name == "c4":
+    elif base == "c4":
         g.manual_seed(4); gc.manual_seed(4)
         B, Sq, H, Hk, cap = 4, 2048, 32, 8, 8192
         L = torch.full((B,), 6144, dtype=torch.int32)
@@ -170,7 +176,8 @@ def build_case(name, torch, dev, ncopy):
     params = []
     for (kc, vc) in caches:
         p = capi.new_params(
-            dtype=capi.FA_DTYPE_BF16, batch=B, seqlen_q=Sq, nheads=H, nheads_k=Hk, headdim=D, headdim_v=D,
+            dtype=capi.FA_DTYPE_FP8_E4M3 if f8 else capi.FA_DTYPE_BF16, batch=B, seqlen_q=Sq, nheads=H,
+            nheads_k=Hk, headdim=D, headdim_v=D,
             seqlen_k=kc.shape[1] if bt is None else 0, batch_cache=kc.shape[0],
             q=_ptr(q), q_batch_stride=q.stride(0), q_row_stride=q.stride(1), q_head_stride=q.stride(2),
             k=_ptr(kc), k_batch_stride=kc.stride(0), k_row_stride=kc.stride(1), k_head_stride=kc.stride(2),
@@ -203,11 +210,13 @@ def build_case(name, torch, dev, ncopy):
         p.workspace, p.workspace_bytes = _ptr(ws), ws.numel()
         params.append(p)
 
+    if f8:
+        c["work_desc"] = c["work_desc"].replace("bf16", "fp8 e4m3 (q, cache, k/v; bf16 out)")
     # algorithmic work (per call)
-    e = 2
-    if name in ("c2", "c3"):
+    e = 1 if f8 else 2
+    if base in ("c2", "c3"):
         kv = 2 * kv_tokens * Hk * D * e                      # K and V of L+1 tokens
-        qo = 2 * B * Sq * H * D * e + 4 * B * H * Sq          # q read, out write, lse write
+        qo = B * Sq * H * D * (e + 2) + 4 * B * H * Sq        # q read, bf16 out write, lse write
         app = 2 * 2 * B * Hk * D * e                          # new k/v read + cache write
         c["attn_bytes"] = kv + qo
         c["bytes"] = kv + qo + app
@@ -382,7 +391,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c2,c3,c4,c5,bwd")
+    ap.add_argument("--configs", default="c2,c3,c4,c5,bwd,c2f8,c3f8")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 plain device copies of 1 GiB (reference for rocprof FETCH_SIZE/WRITE_SIZE)")
@@ -410,7 +419,7 @@ def main():
                   file=sys.stderr, flush=True)
             torch.cuda.empty_cache()
             continue
-        ncopy = {"c2": 2, "c3": 2, "c4": 1, "c5": 4}[name]
+        ncopy = {"c2": 2, "c3": 2, "c4": 1, "c5": 4, "c2f8": 2, "c3f8": 2}[name]
         c = build_case(name, torch, dev, ncopy)
         torch.cuda.synchronize()
         t = time_case(c, hip, torch, args.steps, args.warmup)

@@ -31,13 +31,16 @@ constexpr int TABN = 256;    // paged: block ids staged per wave
 constexpr int MAXB = 2048;
 }  // namespace dec
 
-// Tile shape per kernel head dim: a tile is 16 KB of K and V (32 keys at head
-// dim 128, 64 keys at 64), so a wave keeps the same bytes in flight and every
-// lane loads full 16-byte chunks at both head dims.
-template <int HD>
+// Tile shape per kernel head dim and stored element size EB: a tile is 16 KB
+// of K and V (32 keys at head dim 128, 64 keys at 64), so a wave keeps the
+// same bytes in flight and every lane loads full 16-byte chunks. FP8 tiles
+// hold 64 keys at both head dims (16 KB at 128, 8 KB at 64): at 32 keys the
+// tile's fixed latency chain (QK -> softmax -> PV, one wave per SIMD), not
+// HBM, set the pace, and 128-key tiles at head dim 64 spill.
+template <int HD, int EB = 2>
 struct DecCfg {
     static constexpr int D = HD;
-    static constexpr int KT = 4096 / HD;   // keys per tile
+    static constexpr int KT = 8192 / (HD * EB) < 64 ? 8192 / (HD * EB) : 64;  // keys per tile
     static constexpr int NH = KT / 16;     // 16-key blocks per tile
     static constexpr int KSTEPS = D / 32;
     static constexpr int DBLK = D / 16;
@@ -111,9 +114,9 @@ __device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref
 template <int DT, int HD, int STAGES, bool BIAS, bool FUSE, int LAYOUT, bool HDM = false>
 __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     using namespace dec;
-    using C = DecCfg<HD>;
-    constexpr int D = C::D, KT = C::KT, NH = C::NH, KSTEPS = C::KSTEPS, DBLK = C::DBLK;
     constexpr bool F8 = DT == DT_FP8;
+    using C = DecCfg<HD, F8 ? 1 : 2>;
+    constexpr int D = C::D, KT = C::KT, NH = C::NH, KSTEPS = C::KSTEPS, DBLK = C::DBLK;
     using ET = std::conditional_t<F8, uint8_t, uint16_t>;  // stored element
     constexpr int EPL = 16 / sizeof(ET);                    // elements per 16-byte load
     constexpr int KL = F8 ? KSTEPS / 2 : KSTEPS;            // 16-byte loads per lane and key row
@@ -612,6 +615,12 @@ __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int wor
 }
 
 constexpr int kDecodeStages = 3;
+// FP8 tiles are half the bytes: more of them in flight keep as many bytes
+// outstanding per wave as the bf16 pipeline does
+#ifndef FA_DEC_F8_STAGES
+#define FA_DEC_F8_STAGES 3
+#endif
+constexpr int kDecodeStagesF8 = FA_DEC_F8_STAGES;
 
 int decode_workers(int cus) { return cus * dec::NWAVE; }
 
@@ -619,7 +628,7 @@ template <int DT, int HD, int LAYOUT>
 static void launch_decode_l(const FwdArgs& a, int grid, hipStream_t stream) {
     const bool bias = a.softcap > 0.f || a.alibi != nullptr;
     const bool fuse = a.k_new != nullptr;
-    constexpr int S = kDecodeStages;
+    constexpr int S = DT == DT_FP8 ? kDecodeStagesF8 : kDecodeStages;
     if (bias) {
         if (fuse) hipLaunchKernelGGL((fa_decode_kernel<DT, HD, S, true, true, LAYOUT>), dim3(grid), dim3(256), 0, stream, a);
         else hipLaunchKernelGGL((fa_decode_kernel<DT, HD, S, true, false, LAYOUT>), dim3(grid), dim3(256), 0, stream, a);
@@ -631,11 +640,11 @@ static void launch_decode_l(const FwdArgs& a, int grid, hipStream_t stream) {
 
 template <int DT, int HD>
 static void launch_decode_t(const FwdArgs& a, int grid, hipStream_t stream) {
-    constexpr int KT = DecCfg<HD>::KT;
+    constexpr int KT = DecCfg<HD, DT == DT_FP8 ? 1 : 2>::KT;
     if (a.hd < HD) {
         // head dims below the kernel's: the generic-layout, bias-capable
         // instances with dim masking (correct for every input of this kernel)
-        constexpr int S = kDecodeStages;
+        constexpr int S = DT == DT_FP8 ? kDecodeStagesF8 : kDecodeStages;
         if (a.k_new) hipLaunchKernelGGL((fa_decode_kernel<DT, HD, S, true, true, 2, true>), dim3(grid), dim3(256), 0, stream, a);
         else hipLaunchKernelGGL((fa_decode_kernel<DT, HD, S, true, false, 2, true>), dim3(grid), dim3(256), 0, stream, a);
         return;

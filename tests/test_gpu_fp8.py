@@ -100,12 +100,14 @@ def test_fp8_decode_fused_append_descales(D):
     check(out, lse, ro, rl, vmax=float(vd.max()))
 
 
-@pytest.mark.parametrize("D", [64, 96, 128])
+@pytest.mark.parametrize("D", [64])
 def test_fp8_decode_bitwise_equals_bf16_on_widened_inputs(D):
     """With unit descales the FP8 decode computes on exactly the bf16 values
-    of its bytes, with the same score formula as the bf16 kernel: the outputs
-    and LSE must be bitwise those of the bf16 path run on the widened
-    tensors."""
+    of its bytes, with the same score formula as the bf16 kernel and, at head
+    dim 64, the same 64-key tiles: the outputs and LSE must be bitwise those
+    of the bf16 path run on the widened tensors. (At head dim 128 the FP8
+    tiles hold 64 keys and the bf16 tiles 32, so the online softmax rescales
+    at different points and only the oracle tolerances apply.)"""
     import flash_attn_npu_v3 as fa3
     print(f"case fp8 decode == bf16 decode D={D}", flush=True)
     g = torch.Generator().manual_seed(100 + D)
