@@ -79,6 +79,18 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16(u32x2 r) {
     return o;
 }
 
+// 16x16x128 MFMA on e4m3 operands (gfx950 f8f6f4, format 0 = E4M3 for both,
+// E8M0 scales 127 = 1). Lane l holds A[l%16][32*(l/16)+e] and
+// B[32*(l/16)+e][l%16], e < 32: the 32 bytes of a[0], a[1] (lowest first).
+// The result lane l holds D[4*(l/16)+i][l%16]. Products of e4m3 values are
+// exact in fp32.
+__device__ __forceinline__ f32x4 mfma16x16x128_e4m3(u32x4 a0, u32x4 a1, u32x4 b0, u32x4 b1, f32x4 c) {
+    typedef int i32x8 __attribute__((ext_vector_type(8)));
+    const i32x8 a = {(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+    const i32x8 b = {(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
 // FP8 descale factor of (batch b, kv head hk); a null table means 1.
 __device__ __forceinline__ float descale_at(const float* p, int64_t sb, int64_t sh, int b, int hk) {
     return p ? p[(int64_t)b * sb + (int64_t)hk * sh] : 1.f;

@@ -109,8 +109,10 @@ __device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref
 // HDM: head dim below 128 (dims >= a.hd read as zero, never written).
 // DT_FP8: the cache, q and k_new / v_new hold e4m3fn bytes. The register
 // pipeline carries the raw bytes (half the registers and half the HBM bytes
-// of a bf16 cache); a tile is widened to bf16 when it is consumed, and the
-// descales scale the scores (q_descale * k_descale) and the output (v_descale).
+// of a bf16 cache). S^T = K.Q^T runs as 16x16x128 e4m3 MFMAs on those bytes;
+// V is widened to bf16 on its way into the wave's LDS tile, and P.V stays a
+// bf16 product. The descales scale the scores (q_descale * k_descale) and
+// the output (v_descale).
 template <int DT, int HD, int STAGES, bool BIAS, bool FUSE, int LAYOUT, bool HDM = false>
 __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     using namespace dec;
@@ -264,6 +266,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     // ---- compute side --------------------------------------------------------------------
     DecSeg cs = dec_seg_of(a, s_pref, s_bat, t0);
     u32x4 qreg[KSTEPS];
+    u32x4 q8[2];  // FP8: the raw q bytes of dims G * D / 4 .. + D / 4 (zero-padded to 32)
     float slope = 0.f;
     int qi = 0;
     f32x4 oacc[DBLK];
@@ -284,14 +287,19 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         const ET* qrow = a.cu_seqlens_q
                              ? qp + ((int64_t)a.cu_seqlens_q[s.b] + i) * a.q_si + (int64_t)h * a.q_sh
                              : qp + (int64_t)s.b * a.q_sb + (int64_t)i * a.q_si + (int64_t)h * a.q_sh;
+        if constexpr (F8) {
+            // same bytes per lane as the K loads: B operand of the e4m3 MFMA
 #pragma unroll
-        for (int s2 = 0; s2 < KSTEPS; ++s2) {
-            const bool in = ok && (!HDM || (G * KSTEPS + s2) * 8 < a.hd);
-            if constexpr (F8)
-                qreg[s2] = in ? fp8x8_to_bf16(*reinterpret_cast<const u32x2*>(qrow + (G * KSTEPS + s2) * 8))
-                              : u32x4{0u, 0u, 0u, 0u};
-            else
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const bool in = ok && s2 < KL && (!HDM || G * (D / 4) + s2 * EPL < a.hd);
+                q8[s2] = in ? *reinterpret_cast<const u32x4*>(qrow + G * (D / 4) + s2 * EPL) : u32x4{0u, 0u, 0u, 0u};
+            }
+        } else {
+#pragma unroll
+            for (int s2 = 0; s2 < KSTEPS; ++s2) {
+                const bool in = ok && (!HDM || (G * KSTEPS + s2) * 8 < a.hd);
                 qreg[s2] = in ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s2) * 8) : u32x4{0u, 0u, 0u, 0u};
+            }
         }
         if constexpr (F8) {
             const float qk = descale_at(a.qd, a.qd_sb, a.qd_sh, s.b, s.hk) * descale_at(a.kd, a.kd_sb, a.kd_sh, s.b, s.hk);
@@ -385,10 +393,20 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         f32x4 sacc[NH];
 #pragma unroll
         for (int h = 0; h < NH; ++h) sacc[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (F8) {
+            // one e4m3 MFMA per 16 keys over all dims: lane (li, G) holds key
+            // li's and row li's dims G * D / 4 .. + D / 4, its raw loads (at
+            // head dim 64 the upper 16 bytes are zero on both sides)
 #pragma unroll
-        for (int s = 0; s < KSTEPS; ++s)
+            for (int h = 0; h < NH; ++h)
+                sacc[h] = mfma16x16x128_e4m3(kk[h][0], KL > 1 ? kk[h][KL - 1] : u32x4{0u, 0u, 0u, 0u}, q8[0], q8[1],
+                                             sacc[h]);
+        } else {
 #pragma unroll
-            for (int h = 0; h < NH; ++h) sacc[h] = mfma16x16x32<DT>(opnd(kk, h, s), qreg[s], sacc[h]);
+            for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+                for (int h = 0; h < NH; ++h) sacc[h] = mfma16x16x32<DT>(opnd(kk, h, s), qreg[s], sacc[h]);
+        }
         // online softmax (log2 domain), row = li, keys key0 + 16h + 4G + e
         const int sk = cs.sk, diag0 = cs.sk - cs.sq;
         const bool full = key0 + KT <= sk && key0 >= seg_flo && key0 + KT - 1 <= seg_fhi;
