@@ -224,3 +224,57 @@ def test_fp8_without_descales_and_rejections():
         fa3.flash_attn_func(h.to(DEV), h.to(DEV), h.to(DEV))
     with pytest.raises(RuntimeError, match="dtype"):
         fa3.flash_attn_func(q.to(DEV), k.to(DEV).to(torch.bfloat16), v.to(DEV).to(torch.bfloat16))
+
+
+def test_fp8_paged_prefill_and_ragged_append():
+    """The paged prefill instance (many query rows against a permuted block
+    table) and the ragged append (cu_seqlens_q / cu_seqlens_k_new) on FP8
+    caches, each against the checker on the equivalent contiguous layout."""
+    import flash_attn_npu_v3 as fa3
+    print("case fp8 paged prefill + ragged append", flush=True)
+    g = torch.Generator().manual_seed(21)
+    B, Sq, H, Hk, D, page = 2, 40, 8, 2, 128, 64
+    L = torch.tensor([100, 450], dtype=torch.int32)
+    need = [(int(l) + page - 1) // page for l in L]
+    mb, nblocks = max(need), sum(need) + 1
+    perm = torch.randperm(nblocks, generator=g)
+    bt = torch.zeros((B, mb), dtype=torch.int32)
+    bt[0, :need[0]], bt[1, :need[1]] = perm[:need[0]], perm[need[0]:need[0] + need[1]]
+    kc, vc = fp8((nblocks, page, Hk, D), g), fp8((nblocks, page, Hk, D), g)
+    q = fp8((B, Sq, H, D), g)
+    qd, kd, vd = descales(B, Hk, g)
+    out, lse, *_ = fa3.flash_attn_with_kvcache(q.to(DEV), kc.to(DEV), vc.to(DEV), cache_seqlens=L.to(DEV),
+                                               page_table=bt.to(DEV), q_descale=qd.to(DEV), k_descale=kd.to(DEV),
+                                               v_descale=vd.to(DEV), causal=True, return_softmax_lse=True)
+    kx = u8(kc)[bt.numpy()].reshape(B, mb * page, Hk, D)
+    vx = u8(vc)[bt.numpy()].reshape(B, mb * page, Hk, D)
+    ro, rl = orc.attention_fp8(u8(q), kx, vx, scale=D ** -0.5, q_descale=qd.numpy(), k_descale=kd.numpy(),
+                               v_descale=vd.numpy(), causal=True, seqlens_k=L.numpy(), nthreads=NT)
+    check(out, lse, ro, rl, vmax=float(vd.max()))
+
+    # ragged queries and ragged new tokens appended into a contiguous FP8 cache
+    lq, ln, S = [3, 30], [5, 30], 600
+    Lc = torch.tensor([200, 333], dtype=torch.int32)
+    cq = torch.tensor([0, 3, 33], dtype=torch.int32)
+    cn = torch.tensor([0, 5, 35], dtype=torch.int32)
+    q2 = fp8((sum(lq), H, D), g)
+    kn, vn = fp8((sum(ln), Hk, D), g), fp8((sum(ln), Hk, D), g)
+    kc2, vc2 = fp8((B, S, Hk, D), g), fp8((B, S, Hk, D), g)
+    kc2_d, vc2_d = kc2.to(DEV), vc2.to(DEV)
+    out2, lse2, *_ = fa3.flash_attn_with_kvcache(q2.to(DEV), kc2_d, vc2_d, k=kn.to(DEV), v=vn.to(DEV),
+                                                 cache_seqlens=Lc.to(DEV), cu_seqlens_q=cq.to(DEV),
+                                                 cu_seqlens_k_new=cn.to(DEV), max_seqlen_q=max(lq),
+                                                 q_descale=qd.to(DEV), k_descale=kd.to(DEV), v_descale=vd.to(DEV),
+                                                 causal=True, return_softmax_lse=True)
+    kx2, vx2 = u8(kc2).copy(), u8(vc2).copy()
+    for b in range(B):
+        kx2[b, Lc[b]:Lc[b] + ln[b]] = u8(kn)[cn[b]:cn[b + 1]]
+        vx2[b, Lc[b]:Lc[b] + ln[b]] = u8(vn)[cn[b]:cn[b + 1]]
+    assert np.array_equal(u8(kc2_d), kx2) and np.array_equal(u8(vc2_d), vx2)
+    for b in range(B):
+        qs = slice(int(cq[b]), int(cq[b + 1]))
+        ro, rl = orc.attention_fp8(u8(q2)[None, qs], kx2[b:b + 1], vx2[b:b + 1], scale=D ** -0.5,
+                                   q_descale=qd.numpy()[b:b + 1], k_descale=kd.numpy()[b:b + 1],
+                                   v_descale=vd.numpy()[b:b + 1], causal=True,
+                                   seqlens_k=np.array([int(Lc[b]) + ln[b]]), nthreads=NT)
+        check(out2[qs][None], lse2[:, qs][None], ro, rl, vmax=float(vd.max()))
