@@ -17,6 +17,7 @@
 #include <cstdlib>
 #include <mutex>
 #include <string>
+#include <type_traits>
 
 #include "../../include/fa_mi355x.h"
 #include "fa_kernel_args.h"
@@ -39,7 +40,7 @@ int bwd_row_block(int d);
 
 namespace {
 
-constexpr int kMaxBatch = 2048;   // per-batch plan lives in LDS
+constexpr int kMaxBatch = 2048;   // sequences per attention launch (per-batch plans live in LDS)
 constexpr int kDecodeRows = 16;   // rows per (b, kv head) that take the decode kernel
 
 thread_local std::string g_err;
@@ -106,7 +107,6 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
     FA_CHECK(p->dtype == FA_DTYPE_FP16 || p->dtype == FA_DTYPE_BF16 || f8,
              "FlashAttention only support fp16 and bf16 data type (and fp8 e4m3 inputs in the forward)");
     FA_CHECK(p->batch >= 1, "batch size must be positive");
-    FA_CHECK(p->batch <= kMaxBatch, "batch size %d exceeds the supported maximum %d", p->batch, kMaxBatch);
     if (f8) {
         // 16-byte loads of e4m3 rows: 16-element head-dim chunks and row starts
         FA_CHECK(p->headdim % 16 == 0, "FP8 inputs need a head dimension that is a multiple of 16");
@@ -227,9 +227,11 @@ void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
     }
     const int cus = cu_count();
     pl.rotary = kind == FA_KIND_KVCACHE && p->rotary_cos != nullptr;
+    // batch entries per attention launch (larger batches run in chunks)
+    const int pb = std::min(p->batch, kMaxBatch);
     size_t off = 0;
     pl.off_sched = off;
-    off = align256(off + sizeof(int) * (2 * (size_t)p->batch + 2));
+    off = align256(off + sizeof(int) * (2 * (size_t)pb + 2));
     if (pl.decode) {
         // stream-K decode: one workgroup of 4 wave workers per CU, <= 2 partials per worker
         pl.grid = cus;
@@ -240,7 +242,7 @@ void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
         pl.min_chunk = 0;
     } else {
         const int occ = 2;  // prefill workgroups per CU
-        const int64_t base_bound = (int64_t)p->batch * p->nheads_k * pl.mt_max;
+        const int64_t base_bound = (int64_t)pb * p->nheads_k * pl.mt_max;
         pl.workers = 0;
         pl.target_items = 2 * cus;
         pl.min_chunk = 2 * pl.BN;
@@ -266,25 +268,41 @@ void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
     pl.total = off;
 }
 
-fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
+// Byte offset of batch entry b0 in a batch-strided tensor of esz-byte elements.
+template <typename T>
+T* boff(T* ptr, int64_t b0, int64_t stride, int esz) {
+    if (!ptr) return ptr;
+    using B = std::conditional_t<std::is_const<T>::value, const char, char>;
+    return reinterpret_cast<T*>(reinterpret_cast<B*>(ptr) + b0 * stride * esz);
+}
+
+// The forward. ws / ws_bytes: the scratch the kernels use (the caller's
+// workspace, or the library's static scratch for the no-allocation entry
+// point). Per-batch kernel plans live in LDS, so a call with more than
+// kMaxBatch sequences runs its attention as consecutive launches over batch
+// chunks on the same stream (the KV append runs once, for the whole batch,
+// before them); the chunks reuse one workspace, since each chunk's merge
+// precedes the next chunk's attention on the stream.
+fa_status_t run_forward_ws(const fa_fwd_params* p, int kind, void* stream_v, void* ws_v, size_t ws_bytes) {
     fa_status_t st = validate(p, kind);
     if (st != FA_OK) return st;
     hipStream_t stream = static_cast<hipStream_t>(stream_v);
     Plan pl;
     make_plan(p, kind, pl);
-    if (p->seqlen_q == 0 && kind != FA_KIND_VARLEN) return FA_OK;
     if (pl.total > 0) {
-        if (!p->workspace || p->workspace_bytes < pl.total)
-            return fail(FA_EWORKSPACE, "workspace of %zu bytes required, %zu given", pl.total,
-                        p->workspace ? p->workspace_bytes : (size_t)0);
-        if (reinterpret_cast<uintptr_t>(p->workspace) & 255u)
-            return fail(FA_EWORKSPACE, "workspace must be 256-byte aligned");
+        if (!ws_v || ws_bytes < pl.total)
+            return fail(FA_EWORKSPACE, "workspace of %zu bytes required, %zu given", pl.total, ws_v ? ws_bytes : (size_t)0);
+        if (reinterpret_cast<uintptr_t>(ws_v) & 255u) return fail(FA_EWORKSPACE, "workspace must be 256-byte aligned");
     }
-    char* ws = static_cast<char*>(p->workspace);
+    char* ws = static_cast<char*>(ws_v);
     const bool paged = p->block_table != nullptr;
+    const bool f8 = p->dtype == FA_DTYPE_FP8_E4M3;
+    const int esz = f8 ? 1 : 2;  // bytes per q / k / v element (out is 16-bit)
+    const bool chunked = p->batch > kMaxBatch;
 
     const void* q_ptr = p->q;
     int64_t q_sb = p->q_batch_stride, q_si = p->q_row_stride, q_sh = p->q_head_stride;
+    int q_esz = esz;
 
     auto mark = [&](int i) {
         if (p->stage_events && p->stage_events[i]) (void)hipEventRecord(static_cast<hipEvent_t>(p->stage_events[i]), stream);
@@ -292,8 +310,17 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
     mark(0);
     // Decode without rotary appends inside the attention kernel; otherwise the
     // append (with the key rotation, and for decode the q rotation) runs as
-    // its own launch first. Prefill rotates q inside its q load.
-    const bool fused_append = kind == FA_KIND_KVCACHE && p->k_new && pl.decode && !pl.rotary && !p->cu_seqlens_k_new;
+    // its own launch first. Prefill rotates q inside its q load. The decode
+    // kernel visits only the key tiles some query row sees and writes a new
+    // token from the tile that holds it, so the fused append is used only
+    // where every new token lies in a visited tile: at most seqlen_q new
+    // tokens (the first row sees its own diagonal key), or no left window and
+    // no attention chunk (every tile from key 0 is visited); ragged q (a
+    // sequence may have no query rows, hence no tiles) takes the separate
+    // append, as does a batch run in chunks.
+    const bool local_left = p->window_size_left >= 0 || p->attention_chunk > 0;
+    const bool fused_append = kind == FA_KIND_KVCACHE && p->k_new && pl.decode && !pl.rotary && !p->cu_seqlens_k_new &&
+                              !p->cu_seqlens_q && !chunked && (p->seqlen_new <= p->seqlen_q || !local_left);
     if (kind == FA_KIND_KVCACHE && p->k_new && !fused_append) {
         fa::KvPrepArgs k{};
         k.k_new = p->k_new;
@@ -331,7 +358,7 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
         k.q_sb = p->q_batch_stride;
         k.q_si = p->q_row_stride;
         k.q_sh = p->q_head_stride;
-        k.q_out = pl.rotary && pl.decode ? ws + pl.off_qrot : nullptr;
+        k.q_out = pl.rotary && pl.decode && p->seqlen_q > 0 ? ws + pl.off_qrot : nullptr;
         const bool local = p->window_size_left >= 0 || p->window_size_right >= 0;
         k.q_same_pos = !(p->is_causal || local);
         k.B = p->batch;
@@ -348,135 +375,155 @@ fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
         k.rot_pos = pl.rotary ? p->rotary_seqlens : nullptr;
         hipError_t e = fa::launch_kv_prep(k, p->dtype, stream);
         if (e != hipSuccess) return fail(FA_EHIP, "kv_prep launch failed: %s", hipGetErrorString(e));
-        if (pl.rotary && pl.decode) {
+        if (k.q_out) {
             q_ptr = ws + pl.off_qrot;
             q_sh = p->headdim;
             q_si = (int64_t)p->nheads * p->headdim;
             q_sb = (int64_t)p->seqlen_q * q_si;
+            q_esz = 2;
         }
     }
+    // no query rows: the append above is all the work
+    if (p->seqlen_q == 0 && kind != FA_KIND_VARLEN) {
+        mark(1);
+        mark(2);
+        mark(3);
+        return FA_OK;
+    }
 
-    fa::FwdArgs a{};
-    a.q = q_ptr;
-    a.q_sb = q_sb;
-    a.q_si = q_si;
-    a.q_sh = q_sh;
-    a.k = p->k;
-    a.k_sb = p->k_batch_stride;
-    a.k_si = p->k_row_stride;
-    a.k_sh = p->k_head_stride;
-    a.v = p->v;
-    a.v_sb = p->v_batch_stride;
-    a.v_si = p->v_row_stride;
-    a.v_sh = p->v_head_stride;
-    a.out = p->out;
-    a.o_sb = p->out_batch_stride;
-    a.o_si = p->out_row_stride;
-    a.o_sh = p->out_head_stride;
-    a.lse = p->softmax_lse;
     const bool ragged_q = kind == FA_KIND_VARLEN || (kind == FA_KIND_KVCACHE && p->cu_seqlens_q);
-    if (ragged_q) {
-        a.lse_sb = 0;
-        a.lse_sh = p->total_q;
-    } else {
-        a.lse_sb = (int64_t)p->nheads * p->seqlen_q;
-        a.lse_sh = p->seqlen_q;
-    }
-    a.seqlens_k = kind == FA_KIND_DENSE ? nullptr : p->cache_seqlens;  // kvcache lengths / varlen seqused_k
-    a.cu_seqlens_q = ragged_q ? p->cu_seqlens_q : nullptr;
-    a.cu_seqlens_k = kind == FA_KIND_VARLEN ? p->cu_seqlens_k : nullptr;
-    a.block_table = p->block_table;
-    a.batch_idx = kind == FA_KIND_KVCACHE ? p->cache_batch_idx : nullptr;
-    a.alibi = p->alibi_slopes;
-    a.bt_stride = p->block_table_batch_stride;
-    a.alibi_sb = p->alibi_batch_stride;
-    a.scale = p->softmax_scale;
-    a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
-    a.softcap = p->softcap;
-    a.B = p->batch;
-    a.Sq = p->seqlen_q;
-    a.Sk = kind == FA_KIND_KVCACHE ? pl.kv_capacity : p->seqlen_k;
-    a.H = p->nheads;
-    a.Hk = p->nheads_k;
-    a.g = pl.g;
-    a.hd = p->headdim;
-    a.seqlen_new = (kind == FA_KIND_KVCACHE && p->k_new && !p->cu_seqlens_k_new) ? p->seqlen_new : 0;
-    if (kind == FA_KIND_KVCACHE) {
-        a.leftpad = p->cache_leftpad;
-        a.cu_knew = p->k_new ? p->cu_seqlens_k_new : nullptr;
-        a.rot_pos = pl.rotary ? p->rotary_seqlens : nullptr;
-    }
-    a.chunk = p->attention_chunk;
-    if (p->dtype == FA_DTYPE_FP8_E4M3) {  // descales are read for FP8 inputs only
-        a.qd = p->q_descale;
-        a.qd_sb = p->q_descale_batch_stride;
-        a.qd_sh = p->q_descale_head_stride;
-        a.kd = p->k_descale;
-        a.kd_sb = p->k_descale_batch_stride;
-        a.kd_sh = p->k_descale_head_stride;
-        a.vd = p->v_descale;
-        a.vd_sb = p->v_descale_batch_stride;
-        a.vd_sh = p->v_descale_head_stride;
-    }
-    if (fused_append) {
-        a.k_new = p->k_new;
-        a.kn_sb = p->knew_batch_stride;
-        a.kn_si = p->knew_row_stride;
-        a.kn_sh = p->knew_head_stride;
-        a.v_new = p->v_new;
-        a.vn_sb = p->vnew_batch_stride;
-        a.vn_si = p->vnew_row_stride;
-        a.vn_sh = p->vnew_head_stride;
-    }
-    if (pl.rotary && !pl.decode) {
-        a.rot_cos = p->rotary_cos;
-        a.rot_sin = p->rotary_sin;
-        a.rot_dim = p->rotary_dim;
-        a.rot_interleaved = p->rotary_interleaved ? 1 : 0;
-        a.rot_same_pos = !(p->is_causal || p->window_size_left >= 0 || p->window_size_right >= 0);
-        a.seqlen_ro = p->seqlen_ro;
-    }
-    // window normalisation (flash_api.cpp:483-494): the seqlen-dependent rules
-    // leave the mask unchanged, causal forces the right edge to the diagonal
-    int wl = p->window_size_left < 0 ? -1 : p->window_size_left;
-    int wr = p->window_size_right < 0 ? -1 : p->window_size_right;
-    if (p->is_causal) wr = 0;
-    a.wl = wl;
-    a.wr = wr;
-    a.page = paged ? p->page_block_size : 1;
-    a.bt_rows = p->block_table_rows;
-    a.num_blocks = paged ? p->batch_cache : 0;
-    a.batch_cache = kind == FA_KIND_KVCACHE ? p->batch_cache : p->batch;
-    a.kv_capacity = pl.kv_capacity;
-    a.part_o = pl.allow_split ? reinterpret_cast<float*>(ws + pl.off_po) : nullptr;
-    a.part_lse = pl.allow_split ? reinterpret_cast<float*>(ws + pl.off_plse) : nullptr;
-    a.sched = reinterpret_cast<int*>(ws + pl.off_sched);
-    a.allow_split = pl.allow_split ? 1 : 0;
-    a.num_splits = p->num_splits > 1 ? p->num_splits : 0;
-    a.target_items = pl.target_items;
-    a.min_chunk = pl.min_chunk;
-    a.mt_max = pl.mt_max;
-    a.page_shift = -1;
-    if (paged && (p->page_block_size & (p->page_block_size - 1)) == 0) {
-        int sh = 0;
-        while ((1 << sh) < p->page_block_size) ++sh;
-        a.page_shift = sh;
-    }
-
+    const bool kv_batched = !paged && !p->cache_batch_idx && !(kind == FA_KIND_VARLEN && p->cu_seqlens_k);
     mark(1);
-    hipError_t e = pl.decode ? fa::launch_decode(a, p->dtype, pl.kd, pl.grid, stream)
-                             : fa::launch_fwd(a, p->dtype, pl.kd, pl.grid, stream);
-    if (e != hipSuccess) return fail(FA_EHIP, "attention launch failed: %s", hipGetErrorString(e));
-    mark(2);
-    if (pl.decode) {
-        hipError_t em = fa::launch_decode_merge(a, p->dtype, pl.kd, pl.grid, stream);
-        if (em != hipSuccess) return fail(FA_EHIP, "merge launch failed: %s", hipGetErrorString(em));
-    } else if (pl.allow_split) {
-        hipError_t em = fa::launch_merge(a, p->dtype, pl.kd, stream);
-        if (em != hipSuccess) return fail(FA_EHIP, "merge launch failed: %s", hipGetErrorString(em));
+    for (int b0 = 0; b0 < p->batch; b0 += kMaxBatch) {
+        const int nb = std::min(kMaxBatch, p->batch - b0);
+        fa::FwdArgs a{};
+        a.q = ragged_q ? q_ptr : boff(q_ptr, b0, q_sb, q_esz);
+        a.q_sb = q_sb;
+        a.q_si = q_si;
+        a.q_sh = q_sh;
+        a.k = kv_batched ? boff(p->k, b0, p->k_batch_stride, esz) : p->k;
+        a.k_sb = p->k_batch_stride;
+        a.k_si = p->k_row_stride;
+        a.k_sh = p->k_head_stride;
+        a.v = kv_batched ? boff(p->v, b0, p->v_batch_stride, esz) : p->v;
+        a.v_sb = p->v_batch_stride;
+        a.v_si = p->v_row_stride;
+        a.v_sh = p->v_head_stride;
+        a.out = ragged_q ? p->out : boff(p->out, b0, p->out_batch_stride, 2);
+        a.o_sb = p->out_batch_stride;
+        a.o_si = p->out_row_stride;
+        a.o_sh = p->out_head_stride;
+        if (ragged_q) {
+            a.lse = p->softmax_lse;
+            a.lse_sb = 0;
+            a.lse_sh = p->total_q;
+        } else {
+            a.lse_sb = (int64_t)p->nheads * p->seqlen_q;
+            a.lse_sh = p->seqlen_q;
+            a.lse = p->softmax_lse + (int64_t)b0 * a.lse_sb;
+        }
+        auto at = [&](const int32_t* x) { return x ? x + b0 : x; };
+        a.seqlens_k = kind == FA_KIND_DENSE ? nullptr : at(p->cache_seqlens);  // kvcache lengths / varlen seqused_k
+        a.cu_seqlens_q = ragged_q ? at(p->cu_seqlens_q) : nullptr;  // prefix values stay absolute row offsets
+        a.cu_seqlens_k = kind == FA_KIND_VARLEN ? at(p->cu_seqlens_k) : nullptr;
+        a.batch_idx = kind == FA_KIND_KVCACHE ? at(p->cache_batch_idx) : nullptr;
+        const bool bt_batched = paged && !a.batch_idx;
+        a.block_table = bt_batched ? p->block_table + (int64_t)b0 * p->block_table_batch_stride : p->block_table;
+        a.bt_stride = p->block_table_batch_stride;
+        a.bt_rows = bt_batched ? p->block_table_rows - b0 : p->block_table_rows;
+        a.alibi = p->alibi_slopes ? p->alibi_slopes + (int64_t)b0 * p->alibi_batch_stride : nullptr;
+        a.alibi_sb = p->alibi_batch_stride;
+        a.scale = p->softmax_scale;
+        a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
+        a.softcap = p->softcap;
+        a.B = nb;
+        a.Sq = p->seqlen_q;
+        a.Sk = kind == FA_KIND_KVCACHE ? pl.kv_capacity : p->seqlen_k;
+        a.H = p->nheads;
+        a.Hk = p->nheads_k;
+        a.g = pl.g;
+        a.hd = p->headdim;
+        a.seqlen_new = (kind == FA_KIND_KVCACHE && p->k_new && !p->cu_seqlens_k_new) ? p->seqlen_new : 0;
+        if (kind == FA_KIND_KVCACHE) {
+            a.leftpad = at(p->cache_leftpad);
+            a.cu_knew = p->k_new ? at(p->cu_seqlens_k_new) : nullptr;
+            a.rot_pos = pl.rotary ? at(p->rotary_seqlens) : nullptr;
+        }
+        a.chunk = p->attention_chunk;
+        if (f8) {  // descales are read for FP8 inputs only
+            a.qd = p->q_descale ? p->q_descale + (int64_t)b0 * p->q_descale_batch_stride : nullptr;
+            a.qd_sb = p->q_descale_batch_stride;
+            a.qd_sh = p->q_descale_head_stride;
+            a.kd = p->k_descale ? p->k_descale + (int64_t)b0 * p->k_descale_batch_stride : nullptr;
+            a.kd_sb = p->k_descale_batch_stride;
+            a.kd_sh = p->k_descale_head_stride;
+            a.vd = p->v_descale ? p->v_descale + (int64_t)b0 * p->v_descale_batch_stride : nullptr;
+            a.vd_sb = p->v_descale_batch_stride;
+            a.vd_sh = p->v_descale_head_stride;
+        }
+        if (fused_append) {  // one chunk only
+            a.k_new = p->k_new;
+            a.kn_sb = p->knew_batch_stride;
+            a.kn_si = p->knew_row_stride;
+            a.kn_sh = p->knew_head_stride;
+            a.v_new = p->v_new;
+            a.vn_sb = p->vnew_batch_stride;
+            a.vn_si = p->vnew_row_stride;
+            a.vn_sh = p->vnew_head_stride;
+        }
+        if (pl.rotary && !pl.decode) {
+            a.rot_cos = p->rotary_cos;
+            a.rot_sin = p->rotary_sin;
+            a.rot_dim = p->rotary_dim;
+            a.rot_interleaved = p->rotary_interleaved ? 1 : 0;
+            a.rot_same_pos = !(p->is_causal || p->window_size_left >= 0 || p->window_size_right >= 0);
+            a.seqlen_ro = p->seqlen_ro;
+        }
+        // window normalisation (flash_api.cpp:483-494): the seqlen-dependent rules
+        // leave the mask unchanged, causal forces the right edge to the diagonal
+        int wl = p->window_size_left < 0 ? -1 : p->window_size_left;
+        int wr = p->window_size_right < 0 ? -1 : p->window_size_right;
+        if (p->is_causal) wr = 0;
+        a.wl = wl;
+        a.wr = wr;
+        a.page = paged ? p->page_block_size : 1;
+        a.num_blocks = paged ? p->batch_cache : 0;
+        a.batch_cache = kind == FA_KIND_KVCACHE ? (kv_batched ? p->batch_cache - b0 : p->batch_cache) : nb;
+        a.kv_capacity = pl.kv_capacity;
+        a.part_o = pl.allow_split ? reinterpret_cast<float*>(ws + pl.off_po) : nullptr;
+        a.part_lse = pl.allow_split ? reinterpret_cast<float*>(ws + pl.off_plse) : nullptr;
+        a.sched = reinterpret_cast<int*>(ws + pl.off_sched);
+        a.allow_split = pl.allow_split ? 1 : 0;
+        a.num_splits = p->num_splits > 1 ? p->num_splits : 0;
+        a.target_items = pl.target_items;
+        a.min_chunk = pl.min_chunk;
+        a.mt_max = pl.mt_max;
+        a.page_shift = -1;
+        if (paged && (p->page_block_size & (p->page_block_size - 1)) == 0) {
+            int sh = 0;
+            while ((1 << sh) < p->page_block_size) ++sh;
+            a.page_shift = sh;
+        }
+
+        hipError_t e = pl.decode ? fa::launch_decode(a, p->dtype, pl.kd, pl.grid, stream)
+                                 : fa::launch_fwd(a, p->dtype, pl.kd, pl.grid, stream);
+        if (e != hipSuccess) return fail(FA_EHIP, "attention launch failed: %s", hipGetErrorString(e));
+        if (b0 + nb >= p->batch) mark(2);
+        if (pl.decode) {
+            hipError_t em = fa::launch_decode_merge(a, p->dtype, pl.kd, pl.grid, stream);
+            if (em != hipSuccess) return fail(FA_EHIP, "merge launch failed: %s", hipGetErrorString(em));
+        } else if (pl.allow_split) {
+            hipError_t em = fa::launch_merge(a, p->dtype, pl.kd, stream);
+            if (em != hipSuccess) return fail(FA_EHIP, "merge launch failed: %s", hipGetErrorString(em));
+        }
     }
     mark(3);
     return FA_OK;
+}
+
+fa_status_t run_forward(const fa_fwd_params* p, int kind, void* stream_v) {
+    if (!p) return fail(FA_EINVAL, "params must not be null");
+    return run_forward_ws(p, kind, stream_v, p->workspace, p->workspace ? p->workspace_bytes : 0);
 }
 
 // ---- backward ---------------------------------------------------------------------------
@@ -490,7 +537,6 @@ fa_status_t validate_bwd(const fa_bwd_params* p, int kind) {
     FA_CHECK(p->dtype == FA_DTYPE_FP16 || p->dtype == FA_DTYPE_BF16,
              "FlashAttention only support fp16 and bf16 data type");
     FA_CHECK(p->batch >= 1, "batch size must be positive");
-    FA_CHECK(p->batch <= kMaxBatch, "batch size %d exceeds the supported maximum %d", p->batch, kMaxBatch);
     FA_CHECK(p->nheads >= 1 && p->nheads_k >= 1, "number of heads must be positive");
     FA_CHECK(p->nheads % p->nheads_k == 0, "Number of heads in key/value must divide number of heads in query");
     FA_CHECK(p->headdim >= 1 && p->headdim % 8 == 0, "head dimension must be a positive multiple of 8");
@@ -526,84 +572,95 @@ fa_status_t validate_bwd(const fa_bwd_params* p, int kind) {
     return FA_OK;
 }
 
+// Like the forward, a batch above kMaxBatch runs as consecutive launches over
+// batch chunks (the backward's per-batch item prefix lives in LDS).
 fa_status_t run_backward(const fa_bwd_params* p, int kind, void* stream_v) {
     fa_status_t st = validate_bwd(p, kind);
     if (st != FA_OK) return st;
     if (p->seqlen_q == 0 || (kind == FA_KIND_VARLEN && p->total_q == 0)) return FA_OK;
-    fa::BwdArgs a{};
-    a.q = p->q;
-    a.q_sb = p->q_batch_stride;
-    a.q_si = p->q_row_stride;
-    a.q_sh = p->q_head_stride;
-    a.k = p->k;
-    a.k_sb = p->k_batch_stride;
-    a.k_si = p->k_row_stride;
-    a.k_sh = p->k_head_stride;
-    a.v = p->v;
-    a.v_sb = p->v_batch_stride;
-    a.v_si = p->v_row_stride;
-    a.v_sh = p->v_head_stride;
-    a.out = p->out;
-    a.o_sb = p->out_batch_stride;
-    a.o_si = p->out_row_stride;
-    a.o_sh = p->out_head_stride;
-    a.dout = p->dout;
-    a.do_sb = p->dout_batch_stride;
-    a.do_si = p->dout_row_stride;
-    a.do_sh = p->dout_head_stride;
-    a.dq = p->dq;
-    a.dq_sb = p->dq_batch_stride;
-    a.dq_si = p->dq_row_stride;
-    a.dq_sh = p->dq_head_stride;
-    a.dk = p->dk;
-    a.dk_sb = p->dk_batch_stride;
-    a.dk_si = p->dk_row_stride;
-    a.dk_sh = p->dk_head_stride;
-    a.dv = p->dv;
-    a.dv_sb = p->dv_batch_stride;
-    a.dv_si = p->dv_row_stride;
-    a.dv_sh = p->dv_head_stride;
-    a.lse = p->softmax_lse;
-    a.dsum = p->softmax_d;
-    if (kind == FA_KIND_VARLEN) {
-        a.lse_sb = 0;
-        a.lse_sh = p->total_q;
-    } else {
-        a.lse_sb = (int64_t)p->nheads * p->seqlen_q;
-        a.lse_sh = p->seqlen_q;
-    }
-    a.cu_seqlens_q = kind == FA_KIND_VARLEN ? p->cu_seqlens_q : nullptr;
-    a.cu_seqlens_k = kind == FA_KIND_VARLEN ? p->cu_seqlens_k : nullptr;
-    a.alibi = p->alibi_slopes;
-    a.alibi_sb = p->alibi_batch_stride;
-    a.scale = p->softmax_scale;
-    a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
-    a.softcap = p->softcap;
-    a.B = p->batch;
-    a.Sq = p->seqlen_q;
-    a.Sk = p->seqlen_k;
-    a.H = p->nheads;
-    a.Hk = p->nheads_k;
-    a.g = p->nheads / p->nheads_k;
-    a.hd = p->headdim;
-    a.total_q = p->total_q;
-    // window normalisation as in the forward (flash_api.cpp:483-494)
-    int wl = p->window_size_left < 0 ? -1 : p->window_size_left;
-    int wr = p->window_size_right < 0 ? -1 : p->window_size_right;
-    if (p->is_causal) wr = 0;
-    a.wl = wl;
-    a.wr = wr;
-    a.chunk = p->attention_chunk;
+    const bool var = kind == FA_KIND_VARLEN;
     // kernel head dim (64, 128 or 256); dims above headdim read as zero
     const int kd = p->headdim <= 64 ? 64 : p->headdim <= 128 ? 128 : 256;
-    const int64_t gkv = (int64_t)p->batch * p->nheads_k * ((p->seqlen_k + fa::bwd_key_block(kd) - 1) / fa::bwd_key_block(kd));
-    const int64_t gq = (int64_t)p->batch * p->nheads_k *
-                       (((int64_t)p->seqlen_q * a.g + fa::bwd_row_block(kd) - 1) / fa::bwd_row_block(kd));
-    const int cap = 16 * cu_count();  // the kernels walk their work items in a grid-stride loop
-    const int grid_kv = (int)std::max<int64_t>(1, std::min<int64_t>(gkv, cap));
-    const int grid_q = (int)std::max<int64_t>(1, std::min<int64_t>(gq, cap));
-    hipError_t e = fa::launch_bwd(a, p->dtype, kd, grid_kv, grid_q, static_cast<hipStream_t>(stream_v));
-    if (e != hipSuccess) return fail(FA_EHIP, "backward launch failed: %s", hipGetErrorString(e));
+    for (int b0 = 0; b0 < p->batch; b0 += kMaxBatch) {
+        const int nb = std::min(kMaxBatch, p->batch - b0);
+        // dense tensors move to batch entry b0; varlen rows are addressed by
+        // the (absolute) cu_seqlens prefix values
+        auto bt = [&](auto* ptr, int64_t stride) { return var ? ptr : boff(ptr, b0, stride, 2); };
+        fa::BwdArgs a{};
+        a.q = bt(p->q, p->q_batch_stride);
+        a.q_sb = p->q_batch_stride;
+        a.q_si = p->q_row_stride;
+        a.q_sh = p->q_head_stride;
+        a.k = bt(p->k, p->k_batch_stride);
+        a.k_sb = p->k_batch_stride;
+        a.k_si = p->k_row_stride;
+        a.k_sh = p->k_head_stride;
+        a.v = bt(p->v, p->v_batch_stride);
+        a.v_sb = p->v_batch_stride;
+        a.v_si = p->v_row_stride;
+        a.v_sh = p->v_head_stride;
+        a.out = bt(p->out, p->out_batch_stride);
+        a.o_sb = p->out_batch_stride;
+        a.o_si = p->out_row_stride;
+        a.o_sh = p->out_head_stride;
+        a.dout = bt(p->dout, p->dout_batch_stride);
+        a.do_sb = p->dout_batch_stride;
+        a.do_si = p->dout_row_stride;
+        a.do_sh = p->dout_head_stride;
+        a.dq = bt(p->dq, p->dq_batch_stride);
+        a.dq_sb = p->dq_batch_stride;
+        a.dq_si = p->dq_row_stride;
+        a.dq_sh = p->dq_head_stride;
+        a.dk = bt(p->dk, p->dk_batch_stride);
+        a.dk_sb = p->dk_batch_stride;
+        a.dk_si = p->dk_row_stride;
+        a.dk_sh = p->dk_head_stride;
+        a.dv = bt(p->dv, p->dv_batch_stride);
+        a.dv_sb = p->dv_batch_stride;
+        a.dv_si = p->dv_row_stride;
+        a.dv_sh = p->dv_head_stride;
+        if (var) {
+            a.lse_sb = 0;
+            a.lse_sh = p->total_q;
+            a.lse = p->softmax_lse;
+            a.dsum = p->softmax_d;
+        } else {
+            a.lse_sb = (int64_t)p->nheads * p->seqlen_q;
+            a.lse_sh = p->seqlen_q;
+            a.lse = p->softmax_lse + (int64_t)b0 * a.lse_sb;
+            a.dsum = p->softmax_d + (int64_t)b0 * a.lse_sb;
+        }
+        a.cu_seqlens_q = var ? p->cu_seqlens_q + b0 : nullptr;
+        a.cu_seqlens_k = var ? p->cu_seqlens_k + b0 : nullptr;
+        a.alibi = p->alibi_slopes ? p->alibi_slopes + (int64_t)b0 * p->alibi_batch_stride : nullptr;
+        a.alibi_sb = p->alibi_batch_stride;
+        a.scale = p->softmax_scale;
+        a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
+        a.softcap = p->softcap;
+        a.B = nb;
+        a.Sq = p->seqlen_q;
+        a.Sk = p->seqlen_k;
+        a.H = p->nheads;
+        a.Hk = p->nheads_k;
+        a.g = p->nheads / p->nheads_k;
+        a.hd = p->headdim;
+        a.total_q = p->total_q;
+        // window normalisation as in the forward (flash_api.cpp:483-494)
+        int wl = p->window_size_left < 0 ? -1 : p->window_size_left;
+        int wr = p->window_size_right < 0 ? -1 : p->window_size_right;
+        if (p->is_causal) wr = 0;
+        a.wl = wl;
+        a.wr = wr;
+        a.chunk = p->attention_chunk;
+        const int64_t gkv = (int64_t)nb * p->nheads_k * ((p->seqlen_k + fa::bwd_key_block(kd) - 1) / fa::bwd_key_block(kd));
+        const int64_t gq = (int64_t)nb * p->nheads_k *
+                           (((int64_t)p->seqlen_q * a.g + fa::bwd_row_block(kd) - 1) / fa::bwd_row_block(kd));
+        const int cap = 16 * cu_count();  // the kernels walk their work items in a grid-stride loop
+        const int grid_kv = (int)std::max<int64_t>(1, std::min<int64_t>(gkv, cap));
+        const int grid_q = (int)std::max<int64_t>(1, std::min<int64_t>(gq, cap));
+        hipError_t e = fa::launch_bwd(a, p->dtype, kd, grid_kv, grid_q, static_cast<hipStream_t>(stream_v));
+        if (e != hipSuccess) return fail(FA_EHIP, "backward launch failed: %s", hipGetErrorString(e));
+    }
     return FA_OK;
 }
 

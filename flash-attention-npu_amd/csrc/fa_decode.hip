@@ -54,11 +54,12 @@ struct DecSeg {
     int lo_tile;      // first 32-key tile of the sequence's visible key range
     int sk, sq, crow;
     int lp;           // cache_leftpad: key j is cache row lp + j (contiguous caches)
+    int nf;           // key index of this call's first new token (cache_seqlens - lp)
 };
 
 // Per-batch facts kept in LDS: first tile, key count, query count, cache row.
 struct DecBatch {
-    int lo_tile, sk, sq, crow, lp;
+    int lo_tile, sk, sq, crow, lp, nf;
 };
 
 template <int KT>
@@ -66,6 +67,9 @@ __device__ __forceinline__ void dec_batch(const FwdArgs& a, int b, DecBatch& d, 
     int sq = a.cu_seqlens_q ? a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b] : a.Sq;
     int sk;
     const int lp = a.leftpad ? min(max(a.leftpad[b], 0), a.kv_capacity) : 0;
+    // new tokens sit at keys nf .. nf + seqlen_new - 1; those beyond the
+    // capacity are neither attended nor written (sk is clamped below)
+    d.nf = a.seqlens_k ? a.seqlens_k[b] - lp : 0;
     if (a.seqlens_k) sk = a.seqlens_k[b] + (a.cu_knew ? a.cu_knew[b + 1] - a.cu_knew[b] : a.seqlen_new) - lp;
     else if (a.cu_seqlens_k) sk = a.cu_seqlens_k[b + 1] - a.cu_seqlens_k[b];
     else sk = a.Sk;
@@ -101,6 +105,7 @@ __device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref
     s.sq = d.sq;
     s.crow = d.crow;
     s.lp = d.lp;
+    s.nf = d.nf;
     return s;
 }
 
@@ -213,9 +218,11 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         return base + (int64_t)s.crow * sb + (int64_t)(s.lp + key) * si + (int64_t)s.hk * sh;
     };
 
-    // With a fused append, keys >= sk - seqlen_new come from k_new / v_new; the
+    // With a fused append, keys nf .. sk - 1 come from k_new / v_new; the
     // worker that owns their tile also writes them into the cache (each tile
-    // has exactly one owner, and no other tile reads those positions).
+    // has exactly one owner, and no other tile reads those positions). New
+    // tokens past the cache capacity (nf + seqlen_new > sk) are dropped, as
+    // the separate append kernel drops them.
     constexpr bool fuse = FUSE;
     const ET* knp = static_cast<const ET*>(a.k_new);
     const ET* vnp = static_cast<const ET*>(a.v_new);
@@ -232,7 +239,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             blk = tab[t - tab_base];
         }
         const int key0 = (is.lo_tile + (t - is.S)) * KT;
-        const int first_new = fuse ? is.sk - a.seqlen_new : 0x7fffffff;
+        const int first_new = fuse ? is.nf : 0x7fffffff;
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
             const int key = key0 + h * 16 + li;
@@ -349,9 +356,9 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
 
     auto compute = [&](int t, const u32x4 (&kk)[NH][KL], const u32x4 (&vv)[NH][KL], int blk) {
         const int key0 = (cs.lo_tile + (t - cs.S)) * KT;
-        if (fuse && key0 + KT > cs.sk - a.seqlen_new) {
+        if (fuse && key0 + KT > cs.nf) {
             // this tile holds appended tokens: write them into the cache
-            const int first_new = cs.sk - a.seqlen_new;
+            const int first_new = cs.nf;
             ET* kc = const_cast<ET*>(kp);
             ET* vc = const_cast<ET*>(vp);
 #pragma unroll

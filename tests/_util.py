@@ -6,6 +6,13 @@ from oracle import fa_oracle as orc
 
 TOL = {torch.float16: 2e-3, torch.bfloat16: 1e-2}   # out max-abs vs the fp32 golden
 LSE_RTOL = 1e-4
+# Absolute floor of the LSE check, for |LSE| < 0.1 only (below that the 1e-4
+# relative bound is under 1e-5): a row's LSE is formed from fp32 dot products
+# of bf16 / fp16 values summed in a different order than the golden's, which
+# leaves errors of a few 1e-7 in absolute terms whatever the LSE's size, so a
+# purely relative bound cannot hold for an LSE near zero (e.g. one visible key
+# with a score near 0).
+LSE_ATOL = 1e-5
 
 
 def odt(dtype):
@@ -45,14 +52,18 @@ def assert_close_out(out, ref_bits, dtype, tol=None):
     return mx
 
 
-def assert_close_lse(lse, ref, rtol=LSE_RTOL):
+def assert_close_lse(lse, ref, rtol=LSE_RTOL, atol=LSE_ATOL):
+    """|got - ref| <= rtol * |ref| + atol per row (+inf rows must match);
+    returns the largest relative error |got - ref| / |ref|."""
     got = lse.detach().float().cpu().numpy()
     ref = np.asarray(ref, dtype=np.float32).reshape(got.shape)
     inf_ref = np.isinf(ref)
     assert np.array_equal(np.isinf(got), inf_ref), "LSE +inf pattern differs"
     if (~inf_ref).any():
-        g, r = got[~inf_ref], ref[~inf_ref]
-        rel = np.abs(g - r) / np.maximum(np.abs(r), 1.0)
-        assert float(rel.max()) <= rtol, f"LSE rel {float(rel.max()):.3e} > {rtol:.0e}"
-        return float(rel.max())
+        g, r = got[~inf_ref].astype(np.float64), ref[~inf_ref].astype(np.float64)
+        err = np.abs(g - r)
+        bad = err > rtol * np.abs(r) + atol
+        assert not bad.any(), (f"LSE off by {float(err[bad].max()):.3e} at |ref| = {float(np.abs(r[bad]).min()):.3e} "
+                               f"(bound {rtol:.0e} relative + {atol:.0e})")
+        return float((err / np.maximum(np.abs(r), 1e-30)).max())
     return 0.0

@@ -145,7 +145,6 @@ BAD = [
     (dict(rotary_cos=0x90000, rotary_sin=0xA0000, rotary_dim=64, seqlen_ro=16), 0, "EINVAL",
      "new key / value to be appended"),
     (dict(batch=0), 0, "EINVAL", "batch size"),
-    (dict(batch=4096), 0, "EINVAL", "exceeds"),
     (dict(softcap=-1.0), 0, "EINVAL", "softcap"),
     (dict(batch_cache=1), 0, "EINVAL", "smaller than q batch"),
     (dict(block_table=0xB0000, page_block_size=0, max_blocks_per_seq=1, block_table_rows=2), 0, "EINVAL",
@@ -175,6 +174,18 @@ def test_validate_rejects(capi, over, kind, status, frag):
     st = capi.validate(p, kind)
     assert st == getattr(capi, "FA_" + status), (st, capi.last_error())
     assert frag in capi.last_error()
+
+
+def test_large_batch_accepted(capi):
+    # batches above 2048 run their attention in chunks of launches; the
+    # workspace is sized for one chunk
+    p = _valid(capi, batch=4096, batch_cache=4096)
+    assert capi.validate(p, 0) == capi.FA_OK, capi.last_error()
+    st, big = capi.workspace_size(p, 0)
+    assert st == capi.FA_OK, capi.last_error()
+    p2 = _valid(capi, batch=2048, batch_cache=2048)
+    st, one = capi.workspace_size(p2, 0)
+    assert st == capi.FA_OK and big == one
 
 
 def test_operators_have_meta_shapes():
