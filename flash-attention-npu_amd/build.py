@@ -23,7 +23,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = os.environ.get("FA_MI355X_ARCH", "gfx950")
 
-HIP_SOURCES = ["fa_fwd.hip", "fa_decode.hip", "fa_kv_prep.hip", "fa_bwd.hip", "fa_api.cpp"]
+HIP_SOURCES = ["fa_fwd.hip", "fa_decode.hip", "fa_kv_prep.hip", "fa_bwd.hip", "fa_api.cpp", "fa_noalloc.hip"]
 HIPFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     # no packed fp32 ops (v_pk_*_f32) in any generated code

@@ -666,6 +666,15 @@ fa_status_t run_backward(const fa_bwd_params* p, int kind, void* stream_v) {
 
 }  // namespace
 
+namespace fa {
+// For the no-allocation entry point (fa_noalloc.hip): the kvcache forward on
+// a scratch buffer the library owns, and its error reporting.
+fa_status_t forward_kvcache_on(const fa_fwd_params* p, void* stream, void* scratch, size_t bytes) {
+    return run_forward_ws(p, FA_KIND_KVCACHE, stream, scratch, bytes);
+}
+fa_status_t report_error(fa_status_t st, const char* msg) { return fail(st, "%s", msg); }
+}  // namespace fa
+
 extern "C" {
 
 int fa_abi_version(void) { return FA_MI355X_ABI_VERSION; }

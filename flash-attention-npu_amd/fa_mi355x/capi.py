@@ -17,8 +17,9 @@ FA_DTYPE_FP16, FA_DTYPE_BF16, FA_DTYPE_FP32, FA_DTYPE_FP8_E4M3 = 0, 1, 2, 3
 FA_KIND_KVCACHE, FA_KIND_DENSE, FA_KIND_VARLEN = 0, 1, 2
 
 EXPORTED = ["fa_abi_version", "fa_validate", "fa_fwd_workspace_size", "fa_mha_fwd_kvcache", "fa_mha_fwd",
-            "fa_mha_varlen_fwd", "fa_combine", "fa_last_error", "fa_validate_bwd", "fa_bwd_workspace_size",
-            "fa_mha_bwd", "fa_mha_varlen_bwd"]
+            "fa_mha_varlen_fwd", "fa_mha_fwd_kvcache_noalloc", "fa_combine", "fa_last_error", "fa_validate_bwd",
+            "fa_bwd_workspace_size", "fa_mha_bwd", "fa_mha_varlen_bwd"]
+NOALLOC_SCRATCH_BYTES = 32 << 20  # FA_NOALLOC_SCRATCH_BYTES
 
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
@@ -93,7 +94,7 @@ def lib():
         L.fa_validate.restype = ctypes.c_int
         L.fa_fwd_workspace_size.argtypes = [P, _i32, ctypes.POINTER(ctypes.c_size_t)]
         L.fa_fwd_workspace_size.restype = ctypes.c_int
-        for fn in ("fa_mha_fwd_kvcache", "fa_mha_fwd", "fa_mha_varlen_fwd"):
+        for fn in ("fa_mha_fwd_kvcache", "fa_mha_fwd", "fa_mha_varlen_fwd", "fa_mha_fwd_kvcache_noalloc"):
             getattr(L, fn).argtypes = [P, _vp]
             getattr(L, fn).restype = ctypes.c_int
         L.fa_combine.argtypes = [_vp, _vp, _i32, _i64, _i32, _vp, _i64, _i32, _vp, _vp]
@@ -140,6 +141,11 @@ _ENTRY = {FA_KIND_KVCACHE: "fa_mha_fwd_kvcache", FA_KIND_DENSE: "fa_mha_fwd", FA
 
 def forward(p, kind, stream=0):
     return getattr(lib(), _ENTRY[kind])(ctypes.byref(p), stream)
+
+
+def forward_kvcache_noalloc(p, stream=0):
+    """fa_mha_fwd_kvcache_noalloc: p.workspace is ignored (library scratch)."""
+    return lib().fa_mha_fwd_kvcache_noalloc(ctypes.byref(p), stream)
 
 
 def new_bwd_params(**kw):

@@ -191,6 +191,17 @@ fa_status_t fa_mha_fwd_kvcache(const fa_fwd_params* p, void* stream);
 fa_status_t fa_mha_fwd(const fa_fwd_params* p, void* stream);
 fa_status_t fa_mha_varlen_fwd(const fa_fwd_params* p, void* stream);
 
+/* No-allocation variant of fa_mha_fwd_kvcache. It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). p->workspace is ignored; the kernels' scratch is a device array
+ * of FA_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until the
+ * process ends. A call whose fa_fwd_workspace_size exceeds that limit fails
+ * with FA_EWORKSPACE. Calls that overlap on one GPU share the array and race:
+ * serialise them. Nothing is allocated or freed. */
+#define FA_NOALLOC_SCRATCH_BYTES (32u << 20)
+fa_status_t fa_mha_fwd_kvcache_noalloc(const fa_fwd_params* p, void* stream);
+
 /* Split-KV merge: out_partial (S, R, Dv) fp32, lse_partial (S, R) fp32 ->
  * out (R, Dv) in `out_dtype` (row stride out_row_stride elements),
  * lse (R,) fp32. Rows with no finite partial LSE get out = 0, lse = +inf. */
