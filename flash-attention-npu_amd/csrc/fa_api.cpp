@@ -131,6 +131,13 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
     FA_CHECK(p->num_splits >= 0, "num_splits must be >= 0");
     FA_CHECK(p->attention_chunk >= 0, "attention_chunk must be >= 0");
     FA_CHECK(p->seqlen_q >= 0, "seqlen_q must be >= 0");
+    // packed rows (query position x q head of one kv head) are 32-bit indices in the kernels
+    FA_CHECK((int64_t)p->seqlen_q * (p->nheads / p->nheads_k) <= (int64_t)1 << 30,
+             "seqlen_q * (nheads / nheads_k) must be at most 2^30");
+    // key indices (and tile counts rounded up from them) are 32-bit in the kernels
+    FA_CHECK(p->seqlen_k <= (1 << 30), "seqlen_k must be at most 2^30");
+    FA_CHECK(p->block_table == nullptr || (int64_t)p->max_blocks_per_seq * p->page_block_size <= (int64_t)1 << 30,
+             "block_table columns x page_block_size must be at most 2^30");
     FA_CHECK(p->q && p->k && p->v && p->out && p->softmax_lse, "q, k, v, out and softmax_lse must be given");
     FA_CHECK(aligned16(p->q) && aligned16(p->k) && aligned16(p->v) && aligned16(p->out),
              "q, k, v and out must be 16-byte aligned");
@@ -394,8 +401,8 @@ fa_status_t run_forward_ws(const fa_fwd_params* p, int kind, void* stream_v, voi
     const bool ragged_q = kind == FA_KIND_VARLEN || (kind == FA_KIND_KVCACHE && p->cu_seqlens_q);
     const bool kv_batched = !paged && !p->cache_batch_idx && !(kind == FA_KIND_VARLEN && p->cu_seqlens_k);
     mark(1);
-    for (int b0 = 0; b0 < p->batch; b0 += kMaxBatch) {
-        const int nb = std::min(kMaxBatch, p->batch - b0);
+    for (int64_t b0 = 0; b0 < p->batch; b0 += kMaxBatch) {
+        const int nb = (int)std::min<int64_t>(kMaxBatch, p->batch - b0);
         fa::FwdArgs a{};
         a.q = ragged_q ? q_ptr : boff(q_ptr, b0, q_sb, q_esz);
         a.q_sb = q_sb;
@@ -545,6 +552,9 @@ fa_status_t validate_bwd(const fa_bwd_params* p, int kind) {
     FA_CHECK(p->softcap >= 0.f, "softcap must be non-negative (0.0 disables softcap)");
     FA_CHECK(p->attention_chunk >= 0, "attention_chunk must be >= 0");
     FA_CHECK(p->seqlen_q >= 0 && p->seqlen_k >= 0, "sequence lengths must be >= 0");
+    FA_CHECK((int64_t)p->seqlen_q * (p->nheads / p->nheads_k) <= (int64_t)1 << 30,
+             "seqlen_q * (nheads / nheads_k) must be at most 2^30");
+    FA_CHECK(p->seqlen_k <= (1 << 30), "seqlen_k must be at most 2^30");
     FA_CHECK(p->q && p->k && p->v && p->out && p->dout && p->dq && p->dk && p->dv,
              "q, k, v, out, dout, dq, dk and dv must be given");
     FA_CHECK(p->softmax_lse && p->softmax_d, "softmax_lse and softmax_d must be given");
@@ -581,8 +591,8 @@ fa_status_t run_backward(const fa_bwd_params* p, int kind, void* stream_v) {
     const bool var = kind == FA_KIND_VARLEN;
     // kernel head dim (64, 128 or 256); dims above headdim read as zero
     const int kd = p->headdim <= 64 ? 64 : p->headdim <= 128 ? 128 : 256;
-    for (int b0 = 0; b0 < p->batch; b0 += kMaxBatch) {
-        const int nb = std::min(kMaxBatch, p->batch - b0);
+    for (int64_t b0 = 0; b0 < p->batch; b0 += kMaxBatch) {
+        const int nb = (int)std::min<int64_t>(kMaxBatch, p->batch - b0);
         // dense tensors move to batch entry b0; varlen rows are addressed by
         // the (absolute) cu_seqlens prefix values
         auto bt = [&](auto* ptr, int64_t stride) { return var ? ptr : boff(ptr, b0, stride, 2); };
@@ -652,7 +662,7 @@ fa_status_t run_backward(const fa_bwd_params* p, int kind, void* stream_v) {
         a.wl = wl;
         a.wr = wr;
         a.chunk = p->attention_chunk;
-        const int64_t gkv = (int64_t)nb * p->nheads_k * ((p->seqlen_k + fa::bwd_key_block(kd) - 1) / fa::bwd_key_block(kd));
+        const int64_t gkv = (int64_t)nb * p->nheads_k * (((int64_t)p->seqlen_k + fa::bwd_key_block(kd) - 1) / fa::bwd_key_block(kd));
         const int64_t gq = (int64_t)nb * p->nheads_k *
                            (((int64_t)p->seqlen_q * a.g + fa::bwd_row_block(kd) - 1) / fa::bwd_row_block(kd));
         const int cap = 16 * cu_count();  // the kernels walk their work items in a grid-stride loop

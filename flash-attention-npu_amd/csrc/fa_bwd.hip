@@ -47,12 +47,8 @@ struct BwCfg {
     // K/V operands and dK^T/dV^T accumulators of a wave take ~200 registers,
     // so the kernel runs one wave per SIMD (4 waves, MFMA accumulators in the
     // accumulation registers).
-#ifndef BW_KRB
-#define BW_KRB 1
-#define BW_KNW 8
-#endif
-    static constexpr int KNW = HD > 128 ? 4 : BW_KNW;
-    static constexpr int KRB = HD > 128 ? 1 : HD == 64 ? 2 : BW_KRB;  // 16-key blocks per wave
+    static constexpr int KNW = HD > 128 ? 4 : 8;
+    static constexpr int KRB = HD > 128 ? 1 : HD == 64 ? 2 : 1;  // 16-key blocks per wave
     static constexpr int KNT = KNW * 64;
     static constexpr int BK = KNW * 16 * KRB;
     static constexpr int BQ = 64;

@@ -640,12 +640,9 @@ __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int wor
 }
 
 constexpr int kDecodeStages = 3;
-// FP8 tiles are half the bytes: more of them in flight keep as many bytes
-// outstanding per wave as the bf16 pipeline does
-#ifndef FA_DEC_F8_STAGES
-#define FA_DEC_F8_STAGES 3
-#endif
-constexpr int kDecodeStagesF8 = FA_DEC_F8_STAGES;
+// FP8 tiles hold 64 keys (16 KB at head dim 128), so the bf16 depth keeps as
+// many bytes in flight per wave
+constexpr int kDecodeStagesF8 = 3;
 
 int decode_workers(int cus) { return cus * dec::NWAVE; }
 

@@ -177,10 +177,6 @@ __device__ __forceinline__ const uint16_t* kv_row_ptr(const FwdArgs& a, const ui
 
 
 
-#ifndef PF_RB
-#define PF_RB 2
-#define PF_NW 8
-#endif
 namespace pf {
 constexpr float kLazy = 8.f;       // log2 headroom before the running max moves
 }  // namespace pf
@@ -191,8 +187,8 @@ constexpr float kLazy = 8.f;       // log2 headroom before the running max moves
 template <int HD>
 struct PfCfg {
     static constexpr int D = HD;
-    static constexpr int RB = HD > 128 ? 1 : HD == 64 ? 4 : PF_RB;  // 16-row blocks per wave
-    static constexpr int NW = PF_NW;                  // waves per workgroup
+    static constexpr int RB = HD > 128 ? 1 : HD == 64 ? 4 : 2;  // 16-row blocks per wave
+    static constexpr int NW = 8;                      // waves per workgroup
     static constexpr int NT = NW * 64;
     static constexpr int BM = NW * RB * 16;           // packed rows per work tile
     static constexpr int BN = HD > 128 ? 32 : 64;     // keys per LDS tile (32-key halves)
