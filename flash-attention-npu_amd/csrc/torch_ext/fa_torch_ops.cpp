@@ -1,7 +1,7 @@
 // fa_torch_ops.cpp -- PyTorch-ROCm operators over the C ABI (libfa_mi355x.so).
 //
-// Registers torch.ops.fa_mi355x.{fwd_kvcache, fwd_kvcache_v3, fwd, varlen_fwd, fwd_combine, bwd,
-// varlen_bwd}.
+// Registers torch.ops.fa_mi355x.{fwd_kvcache, fwd_kvcache_v3, fwd, varlen_fwd, fwd_combine,
+// fwd_combine_out, bwd, varlen_bwd}.
 // Argument order and meaning follow the reference pybind entry points
 // (csrc/arch22/flash_attn_npu_v2/flash_api.cpp: mha_fwd_kvcache :356-377,
 // mha_fwd :628-640, mha_varlen_fwd :828-850, bound at :1301-1309). Unlike the
@@ -59,6 +59,27 @@ Tensor workspace_for(const fa_fwd_params& p, int32_t kind, const Tensor& q) {
     return at::empty({(int64_t)std::max<size_t>(bytes, 256)}, q.options().dtype(at::kByte));
 }
 
+// The workspace of a call: the caller's (the region of a v3 scheduler_metadata
+// buffer after its header), checked against what the plan needs, or a fresh
+// one from the caching allocator. Sets p.workspace / p.workspace_bytes.
+Tensor attach_workspace(fa_fwd_params& p, int32_t kind, const Tensor& q, const OptT& given) {
+    Tensor ws;
+    if (given.has_value()) {
+        ws = *given;
+        size_t bytes = 0;
+        check_status(fa_fwd_workspace_size(&p, kind, &bytes));
+        TORCH_CHECK(ws.scalar_type() == at::kByte && ws.is_contiguous(), "scheduler_metadata must be a contiguous uint8 tensor");
+        TORCH_CHECK(ws.device() == q.device(), "scheduler_metadata must be on the device of q");
+        TORCH_CHECK((size_t)ws.numel() >= bytes, "scheduler_metadata was made for a different call: this call needs ",
+                    bytes, " bytes of workspace, the metadata holds ", ws.numel());
+    } else {
+        ws = workspace_for(p, kind, q);
+    }
+    p.workspace = ws.data_ptr();
+    p.workspace_bytes = (size_t)ws.numel();
+    return ws;
+}
+
 void* cur_stream() { return (void*)c10::hip::getCurrentHIPStream().stream(); }
 
 void set_window(fa_fwd_params& p, bool is_causal, int64_t wl, int64_t wr) {
@@ -109,7 +130,8 @@ std::tuple<Tensor, Tensor> kvcache_impl(const Tensor& q, Tensor& kcache, Tensor&
                                         const OptT& rotary_seqlens, double softmax_scale, bool is_causal,
                                         int64_t window_size_left, int64_t window_size_right, int64_t attention_chunk,
                                         double softcap, bool is_rotary_interleaved, int64_t num_splits,
-                                        const OptT& q_descale, const OptT& k_descale, const OptT& v_descale) {
+                                        const OptT& q_descale, const OptT& k_descale, const OptT& v_descale,
+                                        const OptT& workspace) {
     c10::DeviceGuard guard(q.device());
     TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
     check_dev(kcache, q, "k_cache");
@@ -259,9 +281,7 @@ std::tuple<Tensor, Tensor> kvcache_impl(const Tensor& q, Tensor& kcache, Tensor&
         p.out_head_stride = out.stride(2);
     }
     p.softmax_lse = lse.data_ptr<float>();
-    Tensor ws = workspace_for(p, FA_KIND_KVCACHE, q);
-    p.workspace = ws.data_ptr();
-    p.workspace_bytes = (size_t)ws.numel();
+    Tensor ws = attach_workspace(p, FA_KIND_KVCACHE, q, workspace);
     check_status(fa_mha_fwd_kvcache(&p, cur_stream()));
     return {out, lse};
 }
@@ -275,7 +295,7 @@ std::tuple<Tensor, Tensor> fwd_kvcache(const Tensor& q, Tensor& kcache, Tensor& 
     return kvcache_impl(q, kcache, vcache, k_new, v_new, seqlens_k, rotary_cos, rotary_sin, cache_batch_idx,
                         leftpad_k, block_table, alibi_slopes, std::nullopt, std::nullopt, 0, std::nullopt,
                         softmax_scale, is_causal, window_size_left, window_size_right, 0, softcap,
-                        is_rotary_interleaved, num_splits, std::nullopt, std::nullopt, std::nullopt);
+                        is_rotary_interleaved, num_splits, std::nullopt, std::nullopt, std::nullopt, std::nullopt);
 }
 
 std::tuple<Tensor, Tensor> fwd_kvcache_v3(const Tensor& q, Tensor& kcache, Tensor& vcache, const OptT& k_new,
@@ -288,19 +308,20 @@ std::tuple<Tensor, Tensor> fwd_kvcache_v3(const Tensor& q, Tensor& kcache, Tenso
                                           int64_t window_size_left, int64_t window_size_right,
                                           int64_t attention_chunk, double softcap, bool is_rotary_interleaved,
                                           int64_t num_splits, const OptT& q_descale, const OptT& k_descale,
-                                          const OptT& v_descale) {
+                                          const OptT& v_descale, const OptT& workspace) {
     return kvcache_impl(q, kcache, vcache, k_new, v_new, seqlens_k, rotary_cos, rotary_sin, cache_batch_idx,
                         leftpad_k, block_table, alibi_slopes, cu_seqlens_q, cu_seqlens_k_new, max_seqlen_q,
                         rotary_seqlens, softmax_scale, is_causal, window_size_left, window_size_right,
                         attention_chunk, softcap, is_rotary_interleaved, num_splits, q_descale, k_descale,
-                        v_descale);
+                        v_descale, workspace);
 }
 
 // ---- flash_attn_func ------------------------------------------------------------------------
 std::tuple<Tensor, Tensor> fwd(const Tensor& q, const Tensor& k, const Tensor& v, const OptT& alibi_slopes,
                                double p_dropout, double softmax_scale, bool is_causal, int64_t window_size_left,
                                int64_t window_size_right, double softcap, int64_t attention_chunk,
-                               const OptT& q_descale, const OptT& k_descale, const OptT& v_descale) {
+                               const OptT& q_descale, const OptT& k_descale, const OptT& v_descale,
+                               int64_t num_splits, const OptT& workspace) {
     c10::DeviceGuard guard(q.device());
     TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
     check_dev(k, q, "k");
@@ -342,7 +363,8 @@ std::tuple<Tensor, Tensor> fwd(const Tensor& q, const Tensor& k, const Tensor& v
     p.softcap = (float)softcap;
     set_window(p, is_causal, window_size_left, window_size_right);
     p.attention_chunk = (int32_t)attention_chunk;
-    p.num_splits = 0;
+    TORCH_CHECK(num_splits >= 0, "num_splits must be >= 0");
+    p.num_splits = (int32_t)num_splits;
     set_descale(p, q_descale, k_descale, v_descale, q, q.size(0));
     Tensor out = at::empty(q.sizes(), out_options(q));
     Tensor lse = at::empty({q.size(0), q.size(2), q.size(1)}, q.options().dtype(at::kFloat));
@@ -351,9 +373,7 @@ std::tuple<Tensor, Tensor> fwd(const Tensor& q, const Tensor& k, const Tensor& v
     p.out_row_stride = out.stride(1);
     p.out_head_stride = out.stride(2);
     p.softmax_lse = lse.data_ptr<float>();
-    Tensor ws = workspace_for(p, FA_KIND_DENSE, q);
-    p.workspace = ws.data_ptr();
-    p.workspace_bytes = (size_t)ws.numel();
+    Tensor ws = attach_workspace(p, FA_KIND_DENSE, q, workspace);
     check_status(fa_mha_fwd(&p, cur_stream()));
     return {out, lse};
 }
@@ -365,7 +385,8 @@ std::tuple<Tensor, Tensor> varlen_fwd(const Tensor& q, const Tensor& k, const Te
                                       int64_t max_seqlen_q, int64_t max_seqlen_k, double p_dropout,
                                       double softmax_scale, bool is_causal, int64_t window_size_left,
                                       int64_t window_size_right, double softcap, int64_t attention_chunk,
-                                      const OptT& q_descale, const OptT& k_descale, const OptT& v_descale) {
+                                      const OptT& q_descale, const OptT& k_descale, const OptT& v_descale,
+                                      int64_t num_splits, const OptT& workspace) {
     c10::DeviceGuard guard(q.device());
     TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
     check_dev(k, q, "k");
@@ -432,7 +453,8 @@ std::tuple<Tensor, Tensor> varlen_fwd(const Tensor& q, const Tensor& k, const Te
     p.softcap = (float)softcap;
     set_window(p, is_causal, window_size_left, window_size_right);
     p.attention_chunk = (int32_t)attention_chunk;
-    p.num_splits = 0;
+    TORCH_CHECK(num_splits >= 0, "num_splits must be >= 0");
+    p.num_splits = (int32_t)num_splits;
     set_descale(p, q_descale, k_descale, v_descale, q, p.batch);
     Tensor out = at::empty(q.sizes(), out_options(q));
     Tensor lse = at::empty({q.size(1), q.size(0)}, q.options().dtype(at::kFloat));
@@ -441,16 +463,30 @@ std::tuple<Tensor, Tensor> varlen_fwd(const Tensor& q, const Tensor& k, const Te
     p.out_row_stride = out.stride(0);
     p.out_head_stride = out.stride(1);
     p.softmax_lse = lse.data_ptr<float>();
-    Tensor ws = workspace_for(p, FA_KIND_VARLEN, q);
-    p.workspace = ws.data_ptr();
-    p.workspace_bytes = (size_t)ws.numel();
+    Tensor ws = attach_workspace(p, FA_KIND_VARLEN, q, workspace);
     check_status(fa_mha_varlen_fwd(&p, cur_stream()));
     return {out, lse};
 }
 
 // ---- flash_attn_combine --------------------------------------------------------------------------
-std::tuple<Tensor, Tensor> fwd_combine(const Tensor& out_partial, const Tensor& lse_partial, const OptT& out_,
+// combine_into writes the merged rows into `out`; fwd_combine allocates it,
+// fwd_combine_out takes the caller's (declared as written by the op).
+Tensor combine_into(const Tensor& out_partial, const Tensor& lse_partial, Tensor& out);
+
+std::tuple<Tensor, Tensor> fwd_combine(const Tensor& out_partial, const Tensor& lse_partial,
                                        std::optional<at::ScalarType> out_dtype) {
+    TORCH_CHECK(out_partial.dim() >= 2, "out_partial must have a split dimension and headdim_v");
+    std::vector<int64_t> oshape(out_partial.sizes().begin() + 1, out_partial.sizes().end());
+    Tensor out = at::empty(oshape, out_partial.options().dtype(out_dtype.has_value() ? *out_dtype : at::kFloat));
+    Tensor lse = combine_into(out_partial, lse_partial, out);
+    return {out, lse};
+}
+
+Tensor fwd_combine_out(const Tensor& out_partial, const Tensor& lse_partial, Tensor& out) {
+    return combine_into(out_partial, lse_partial, out);
+}
+
+Tensor combine_into(const Tensor& out_partial, const Tensor& lse_partial, Tensor& out) {
     c10::DeviceGuard guard(out_partial.device());
     TORCH_CHECK(out_partial.is_cuda() && lse_partial.is_cuda(), "inputs must be on a GPU device");
     TORCH_CHECK(out_partial.scalar_type() == at::kFloat && lse_partial.scalar_type() == at::kFloat,
@@ -465,9 +501,7 @@ std::tuple<Tensor, Tensor> fwd_combine(const Tensor& out_partial, const Tensor& 
     const int64_t S = po.size(0);
     const int64_t Dv = po.size(-1);
     const int64_t R = S > 0 ? po.numel() / (S * Dv) : 0;
-    at::ScalarType odt = out_dtype.has_value() ? *out_dtype : at::kFloat;
-    std::vector<int64_t> oshape(po.sizes().begin() + 1, po.sizes().end());
-    Tensor out = out_.has_value() ? *out_ : at::empty(oshape, po.options().dtype(odt));
+    TORCH_CHECK(out.device() == po.device(), "out must be on the device of out_partial");
     TORCH_CHECK(out.is_contiguous() && out.numel() == R * Dv, "out must be contiguous with ", R * Dv, " elements");
     int32_t code = out.scalar_type() == at::kFloat ? FA_DTYPE_FP32
                    : out.scalar_type() == at::kBFloat16 ? FA_DTYPE_BF16
@@ -477,7 +511,7 @@ std::tuple<Tensor, Tensor> fwd_combine(const Tensor& out_partial, const Tensor& 
     Tensor lse = at::empty(lshape, po.options());
     check_status(fa_combine(po.data_ptr<float>(), pl.data_ptr<float>(), (int32_t)S, R, (int32_t)Dv, out.data_ptr(), Dv,
                             code, lse.data_ptr<float>(), cur_stream()));
-    return {out, lse};
+    return lse;
 }
 
 // ---- backward (flash_attn_func / flash_attn_varlen_func autograd) ------------------------------
@@ -655,21 +689,23 @@ TORCH_LIBRARY(fa_mi355x, m) {
     m.def(
         "fwd(Tensor q, Tensor k, Tensor v, Tensor? alibi_slopes, float p_dropout, float softmax_scale, bool is_causal, "
         "int window_size_left, int window_size_right, float softcap, int attention_chunk=0, Tensor? q_descale=None, "
-        "Tensor? k_descale=None, Tensor? v_descale=None) -> (Tensor, Tensor)");
+        "Tensor? k_descale=None, Tensor? v_descale=None, int num_splits=0, Tensor? workspace=None) -> (Tensor, Tensor)");
     m.def(
         "fwd_kvcache_v3(Tensor q, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor? k, Tensor? v, Tensor? seqlens_k, "
         "Tensor? rotary_cos, Tensor? rotary_sin, Tensor? cache_batch_idx, Tensor? leftpad_k, Tensor? block_table, "
         "Tensor? alibi_slopes, Tensor? cu_seqlens_q, Tensor? cu_seqlens_k_new, int max_seqlen_q, "
         "Tensor? rotary_seqlens, float softmax_scale, bool is_causal, int window_size_left, int window_size_right, "
         "int attention_chunk, float softcap, bool is_rotary_interleaved, int num_splits, Tensor? q_descale=None, "
-        "Tensor? k_descale=None, Tensor? v_descale=None) -> (Tensor, Tensor)");
+        "Tensor? k_descale=None, Tensor? v_descale=None, Tensor? workspace=None) -> (Tensor, Tensor)");
     m.def(
         "varlen_fwd(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor? cu_seqlens_k, Tensor? seqused_k, "
         "Tensor? block_table, "
         "Tensor? alibi_slopes, int max_seqlen_q, int max_seqlen_k, float p_dropout, float softmax_scale, "
         "bool is_causal, int window_size_left, int window_size_right, float softcap, int attention_chunk=0, "
-        "Tensor? q_descale=None, Tensor? k_descale=None, Tensor? v_descale=None) -> (Tensor, Tensor)");
-    m.def("fwd_combine(Tensor out_partial, Tensor lse_partial, Tensor? out, ScalarType? out_dtype) -> (Tensor, Tensor)");
+        "Tensor? q_descale=None, Tensor? k_descale=None, Tensor? v_descale=None, int num_splits=0, "
+        "Tensor? workspace=None) -> (Tensor, Tensor)");
+    m.def("fwd_combine(Tensor out_partial, Tensor lse_partial, ScalarType? out_dtype) -> (Tensor, Tensor)");
+    m.def("fwd_combine_out(Tensor out_partial, Tensor lse_partial, Tensor(a!) out) -> Tensor");
     m.def(
         "bwd(Tensor dout, Tensor q, Tensor k, Tensor v, Tensor out, Tensor softmax_lse, Tensor? alibi_slopes, "
         "float p_dropout, float softmax_scale, bool is_causal, int window_size_left, int window_size_right, "
@@ -687,6 +723,7 @@ TORCH_LIBRARY_IMPL(fa_mi355x, CUDA, m) {
     m.impl("fwd", &fwd);
     m.impl("varlen_fwd", &varlen_fwd);
     m.impl("fwd_combine", &fwd_combine);
+    m.impl("fwd_combine_out", &fwd_combine_out);
     m.impl("bwd", &bwd);
     m.impl("varlen_bwd", &varlen_bwd);
 }

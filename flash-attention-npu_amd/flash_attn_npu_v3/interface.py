@@ -38,12 +38,129 @@ def _empty_accum(out):
     return e, e
 
 
-def _check_metadata(scheduler_metadata, device):
-    # The split-KV plan is made on the device from cache_seqlens inside the
-    # attention kernel, so a precomputed plan only has to describe the same
-    # problem; results are identical with or without it.
-    if scheduler_metadata is not None and scheduler_metadata.device != device:
+# ---- scheduler metadata -------------------------------------------------------------------------
+# get_scheduler_metadata (interface_arch22.py:1098-1138 of the reference) returns
+# the plan of a later call: here a uint8 device buffer of a 256-byte header
+# (the problem descriptor below, int32) followed by the call's workspace, sized
+# by the library's planner (fa_fwd_workspace_size). A v3 call given the buffer
+# checks that it describes the call (raising otherwise), takes the split count
+# from it (as the reference takes its split plan from the metadata,
+# flash_api.cpp:249-269) and runs on its workspace, so it allocates no scratch.
+# The per-sequence split itself is still decided on the device from
+# cache_seqlens, so the results equal those of the same call without metadata.
+# The buffer is the call's scratch: calls that use one buffer must not overlap
+# (one stream, or ordered streams).
+_MD_TAG = 0x46414D44  # "FAMD"
+_MD_VERSION = 1
+_MD_HEADER = 256
+_MD_FIELDS = ("batch", "max_seqlen_q", "max_seqlen_k", "nheads", "nheads_k", "headdim", "headdim_v", "dtype",
+              "causal", "window_left", "window_right", "attention_chunk", "softcap", "num_splits", "page_size",
+              "varlen_q", "workspace_bytes")
+# fields a call must match; max_seqlen_q bounds the call's query length
+_MD_CHECKED = ("batch", "nheads", "nheads_k", "headdim", "headdim_v", "dtype", "causal", "window_left",
+               "window_right", "attention_chunk", "softcap", "page_size", "varlen_q")
+
+
+def _dtype_code(dt):
+    codes = {torch.float16: 0, torch.bfloat16: 1, torch.float8_e4m3fn: 3}
+    if dt not in codes:
+        raise RuntimeError("FlashAttention only support fp16 and bf16 data type")
+    return codes[dt]
+
+
+def _describe(batch, max_seqlen_q, max_seqlen_k, nheads, nheads_k, headdim, headdim_v, dtype, causal, window_size,
+              attention_chunk, softcap, num_splits, page_size, varlen_q):
+    wl = -1 if window_size[0] < 0 else int(window_size[0])
+    wr = -1 if window_size[1] < 0 else int(window_size[1])
+    if causal:
+        wr = 0
+    return dict(batch=int(batch), max_seqlen_q=int(max_seqlen_q), max_seqlen_k=int(max_seqlen_k), nheads=int(nheads),
+                nheads_k=int(nheads_k), headdim=int(headdim), headdim_v=int(headdim_v), dtype=_dtype_code(dtype),
+                causal=int(bool(causal)), window_left=wl, window_right=wr, attention_chunk=int(attention_chunk),
+                softcap=int(bool(softcap)), num_splits=int(num_splits), page_size=int(page_size or 0),
+                varlen_q=int(bool(varlen_q)), workspace_bytes=0)
+
+
+def _plan_workspace(d):
+    """Largest workspace any call of this description needs (the kvcache call
+    with rotary included), from the library's own planner."""
+    from fa_mi355x import capi
+    B, Sq, Sk, H, Hk, D = d["batch"], max(d["max_seqlen_q"], 1), max(d["max_seqlen_k"], 1), d["nheads"], \
+        d["nheads_k"], d["headdim"]
+    dummy = 1 << 20  # aligned stand-in addresses: the planner never dereferences them
+    common = dict(dtype=d["dtype"], batch=B, seqlen_q=Sq, nheads=H, nheads_k=Hk, headdim=D, headdim_v=d["headdim_v"],
+                  q=dummy, q_batch_stride=Sq * H * D, q_row_stride=H * D, q_head_stride=D,
+                  k=dummy, k_batch_stride=Sk * Hk * D, k_row_stride=Hk * D, k_head_stride=D,
+                  v=dummy, v_batch_stride=Sk * Hk * D, v_row_stride=Hk * D, v_head_stride=D,
+                  out=dummy, out_batch_stride=Sq * H * D, out_row_stride=H * D, out_head_stride=D,
+                  softmax_lse=dummy, softmax_scale=1.0, is_causal=d["causal"],
+                  window_size_left=d["window_left"], window_size_right=d["window_right"],
+                  attention_chunk=d["attention_chunk"], softcap=1.0 if d["softcap"] else 0.0,
+                  num_splits=d["num_splits"])
+    if d["varlen_q"]:
+        common.update(cu_seqlens_q=dummy, total_q=B * Sq)
+    cands = []
+    page = d["page_size"]
+    kv = dict(cache_seqlens=dummy, seqlen_k=Sk, batch_cache=B)
+    if page:
+        nper = (Sk + page - 1) // page
+        kv = dict(cache_seqlens=dummy, block_table=dummy, block_table_batch_stride=nper, max_blocks_per_seq=nper,
+                  block_table_rows=B, page_block_size=page, batch_cache=B * nper, seqlen_k=0)
+    cands.append((capi.FA_KIND_KVCACHE, dict(common, **kv)))
+    if d["dtype"] != 3 and D >= 16:
+        cands.append((capi.FA_KIND_KVCACHE, dict(common, **kv, k_new=dummy, v_new=dummy, seqlen_new=1,
+                                                 knew_batch_stride=Hk * D, knew_row_stride=Hk * D,
+                                                 knew_head_stride=D, vnew_batch_stride=Hk * D,
+                                                 vnew_row_stride=Hk * D, vnew_head_stride=D, rotary_cos=dummy,
+                                                 rotary_sin=dummy, rotary_dim=16, seqlen_ro=Sk)))
+    if not page:
+        cands.append((capi.FA_KIND_DENSE, dict(common, seqlen_k=Sk, batch_cache=B)))
+    cands.append((capi.FA_KIND_VARLEN, dict(common, cu_seqlens_q=dummy, cu_seqlens_k=dummy, total_q=B * Sq,
+                                            seqlen_k=Sk, batch_cache=B)))
+    need = None
+    for kind, kw in cands:
+        st, n = capi.workspace_size(capi.new_params(**kw), kind)
+        if st == capi.FA_OK:
+            need = n if need is None else max(need, n)
+    if need is None:
+        raise RuntimeError("get_scheduler_metadata: " + capi.last_error())
+    return need
+
+
+def _header_tensor(d):
+    vals = [_MD_TAG, _MD_VERSION] + [d[f] for f in _MD_FIELDS]
+    h = torch.zeros(_MD_HEADER // 4, dtype=torch.int32)
+    h[:len(vals)] = torch.tensor(vals, dtype=torch.int64).to(torch.int32)
+    return h.view(torch.uint8)
+
+
+def _read_header(md):
+    h = md[:_MD_HEADER].cpu().view(torch.int32).tolist()
+    if h[0] != _MD_TAG or h[1] != _MD_VERSION:
+        raise RuntimeError("scheduler_metadata does not come from get_scheduler_metadata")
+    return dict(zip(_MD_FIELDS, h[2:2 + len(_MD_FIELDS)]))
+
+
+def _metadata_for(scheduler_metadata, call, device):
+    """The workspace region of `scheduler_metadata` and its split count, after
+    checking that it describes `call`; (None, None) without metadata."""
+    md = scheduler_metadata
+    if md is None:
+        return None, None
+    if not isinstance(md, torch.Tensor) or md.dtype != torch.uint8 or md.dim() != 1 or not md.is_contiguous() \
+            or md.numel() < _MD_HEADER:
+        raise RuntimeError("scheduler_metadata must be the uint8 tensor get_scheduler_metadata returns")
+    if md.device != device:
         raise RuntimeError("scheduler_metadata must be on the same device as q")
+    d = getattr(md, "_fa_metadata", None)
+    if d is None:  # a copy: read the header back (this synchronises, as the reference does)
+        d = _read_header(md)
+    bad = [f"{f} {d[f]} != {call[f]}" for f in _MD_CHECKED if d[f] != call[f]]
+    if call["max_seqlen_q"] > d["max_seqlen_q"]:
+        bad.append(f"max_seqlen_q {call['max_seqlen_q']} > {d['max_seqlen_q']}")
+    if bad:
+        raise RuntimeError("scheduler_metadata was made for a different call: " + ", ".join(bad))
+    return md[_MD_HEADER:], d["num_splits"]
 
 
 def _cu_from_lengths(lengths):
@@ -59,11 +176,15 @@ class FlashAttnFunc(torch.autograd.Function):
         _reject(qv=qv)
         if softmax_scale is None:
             softmax_scale = q.shape[-1] ** (-0.5)
-        _check_metadata(scheduler_metadata, q.device)
+        call = _describe(q.shape[0], q.shape[1], k.shape[1], q.shape[2], k.shape[2], q.shape[3], v.shape[3], q.dtype,
+                         causal, window_size, attention_chunk, softcap, num_splits, 0, False)
+        ws, md_splits = _metadata_for(scheduler_metadata, call, q.device)
+        if md_splits is not None:
+            num_splits = md_splits
         q, k, v = [maybe_contiguous(x) for x in (q, k, v)]
         out, softmax_lse = ops.fwd(q, k, v, None, 0.0, float(softmax_scale), bool(causal), int(window_size[0]),
                                    int(window_size[1]), float(softcap), int(attention_chunk), q_descale, k_descale,
-                                   v_descale)
+                                   v_descale, int(num_splits), ws)
         if any(x.requires_grad for x in (q, k, v)):
             ctx.save_for_backward(q, k, v, out, softmax_lse)
             ctx.softmax_scale = softmax_scale
@@ -93,12 +214,16 @@ class FlashAttnVarlenFunc(torch.autograd.Function):
         _reject(seqused_q=seqused_q, qv=qv)
         if softmax_scale is None:
             softmax_scale = q.shape[-1] ** (-0.5)
-        _check_metadata(scheduler_metadata, q.device)
+        call = _describe(cu_seqlens_q.numel() - 1, max_seqlen_q, max_seqlen_k, q.shape[1], k.shape[1], q.shape[2],
+                         v.shape[2], q.dtype, causal, window_size, attention_chunk, softcap, num_splits, 0, True)
+        ws, md_splits = _metadata_for(scheduler_metadata, call, q.device)
+        if md_splits is not None:
+            num_splits = md_splits
         q, k, v = [maybe_contiguous(x) for x in (q, k, v)]
         out, softmax_lse = ops.varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, None, None,
                                           int(max_seqlen_q), int(max_seqlen_k), 0.0, float(softmax_scale),
                                           bool(causal), int(window_size[0]), int(window_size[1]), float(softcap),
-                                          int(attention_chunk), q_descale, k_descale, v_descale)
+                                          int(attention_chunk), q_descale, k_descale, v_descale, int(num_splits), ws)
         if any(x.requires_grad for x in (q, k, v)):
             ctx.save_for_backward(q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k)
             ctx.has_seqused_k = seqused_k is not None
@@ -151,8 +276,11 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
 def flash_attn_combine(out_partial, lse_partial, out=None, out_dtype=None):
     """Merge split-KV partials: out_partial (num_splits, ..., headdim_v) fp32 and
     lse_partial (num_splits, ...) fp32 -> (out, lse) with
-    lse = log sum_s exp(lse_s) and out = sum_s exp(lse_s - lse) out_s."""
-    return ops.fwd_combine(out_partial, lse_partial, out, out_dtype)
+    lse = log sum_s exp(lse_s) and out = sum_s exp(lse_s - lse) out_s. With
+    `out` given, the merged rows are written into it (fp32, bf16 or fp16)."""
+    if out is not None:
+        return out, ops.fwd_combine_out(out_partial, lse_partial, out)
+    return ops.fwd_combine(out_partial, lse_partial, out_dtype)
 
 
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None, rotary_cos=None, rotary_sin=None,
@@ -192,7 +320,16 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None, rotary
     if cache_seqlens is not None and isinstance(cache_seqlens, int):
         cache_seqlens = torch.full((batch,), cache_seqlens, dtype=torch.int32, device=k_cache.device)
     cache_seqlens = maybe_contiguous(cache_seqlens)
-    _check_metadata(scheduler_metadata, q.device)
+    paged = page_table is not None
+    packed = cu_seqlens_q is not None and not paged and k_cache.dim() == 3
+    sq = int(max_seqlen_q) if cu_seqlens_q is not None and max_seqlen_q is not None else q.shape[-3]
+    cap = k_cache.shape[0] if packed else (page_table.shape[1] * k_cache.shape[1] if paged else k_cache.shape[1])
+    call = _describe(batch, sq, cap, q.shape[-2], k_cache.shape[-2], q.shape[-1], v_cache.shape[-1], q.dtype, causal,
+                     window_size, attention_chunk, softcap, num_splits, k_cache.shape[1] if paged else 0,
+                     cu_seqlens_q is not None)
+    ws, md_splits = _metadata_for(scheduler_metadata, call, q.device)
+    if md_splits is not None:
+        num_splits = md_splits
     q, k, v = [maybe_contiguous(x) for x in (q, k, v)]
     if cu_seqlens_q is not None and max_seqlen_q is None:
         raise RuntimeError("max_seqlen_q is required with cu_seqlens_q")
@@ -208,7 +345,7 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None, rotary
         out, softmax_lse = ops.varlen_fwd(q, k_cache, v_cache, cu_seqlens_q, cu_k, cache_seqlens, None, None,
                                           int(max_seqlen_q), int(k_cache.shape[0]), 0.0, float(softmax_scale),
                                           bool(causal), int(window_size[0]), int(window_size[1]), float(softcap),
-                                          int(attention_chunk), q_descale, k_descale, v_descale)
+                                          int(attention_chunk), q_descale, k_descale, v_descale, int(num_splits), ws)
     else:
         # (batch, seqlen) or ragged (total_q) queries against a (batch_cache,
         # seqlen_cache) or paged cache, with the in-place append of k / v
@@ -221,7 +358,7 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None, rotary
                                               float(softmax_scale), bool(causal), int(window_size[0]),
                                               int(window_size[1]), int(attention_chunk), float(softcap),
                                               bool(rotary_interleaved), int(num_splits), q_descale, k_descale,
-                                              v_descale)
+                                              v_descale, ws)
     if return_softmax_lse:
         oa, la = _empty_accum(out)
         return out, softmax_lse, oa, la
@@ -235,15 +372,20 @@ def get_scheduler_metadata(batch_size, max_seqlen_q, max_seqlen_k, num_heads_q, 
                            cache_leftpad: Optional[torch.Tensor] = None, page_size: Optional[int] = None,
                            max_seqlen_k_new=0, causal=False, window_size=(-1, -1), attention_chunk=0,
                            has_softcap=False, num_splits=0, pack_gqa=None, sm_margin=0):
-    """Describes the problem for a later flash_attn_with_kvcache call.
-
-    On MI355X the split-KV plan is computed by the attention kernel itself from
-    cache_seqlens (no host synchronisation), so the metadata is a small int32
-    descriptor of the problem shape on the device of cache_seqlens; passing it
-    back does not change results (the reference contract:
-    tests/test_flash_attn_npu_v3_metadata.py)."""
+    """The plan of a later flash_attn_with_kvcache / flash_attn_func /
+    flash_attn_varlen_func call (same keywords as the reference,
+    interface_arch22.py:1098-1138): a uint8 tensor on the device of
+    cache_seqlens holding the call's descriptor and its workspace (see the
+    scheduler-metadata notes above). A call given it raises when it describes
+    a different problem."""
     if headdim_v is None:
         headdim_v = headdim
-    desc = [1, batch_size, max_seqlen_q, max_seqlen_k, num_heads_q, num_heads_kv, headdim, headdim_v,
-            int(bool(causal)), int(window_size[0]), int(window_size[1]), int(num_splits), page_size or 0]
-    return torch.tensor(desc, dtype=torch.int32, device=cache_seqlens.device)
+    if num_splits < 0:
+        raise RuntimeError("num_splits must be >= 0")
+    d = _describe(batch_size, max_seqlen_q, max_seqlen_k, num_heads_q, num_heads_kv, headdim, headdim_v, qkv_dtype,
+                  causal, window_size, attention_chunk, has_softcap, num_splits, page_size, cu_seqlens_q is not None)
+    d["workspace_bytes"] = _plan_workspace(d)
+    md = torch.empty((_MD_HEADER + d["workspace_bytes"],), dtype=torch.uint8, device=cache_seqlens.device)
+    md[:_MD_HEADER].copy_(_header_tensor(d))
+    md._fa_metadata = d
+    return md

@@ -206,8 +206,18 @@ def test_operators_have_meta_shapes():
     assert o.shape == qv.shape and l.shape == (8, 10)
     op = torch.empty(4, 2, 3, 8, 128, dtype=torch.float32, device=m)
     lp = torch.empty(4, 2, 3, 8, dtype=torch.float32, device=m)
-    o, l = ops.fwd_combine(op, lp, None, torch.bfloat16)
+    o, l = ops.fwd_combine(op, lp, torch.bfloat16)
     assert o.shape == (2, 3, 8, 128) and o.dtype == torch.bfloat16 and l.shape == (2, 3, 8)
+    l = ops.fwd_combine_out(op, lp, torch.empty(2, 3, 8, 128, dtype=torch.float16, device=m))
+    assert l.shape == (2, 3, 8) and l.dtype == torch.float32
+    # FP8 (e4m3) inputs give a bf16 out in every forward op, v2 kvcache included
+    q8 = torch.empty(2, 3, 8, 128, dtype=torch.float8_e4m3fn, device=m)
+    k8 = torch.empty(2, 64, 2, 128, dtype=torch.float8_e4m3fn, device=m)
+    o, _ = ops.fwd_kvcache(q8, k8, k8, None, None, None, None, None, None, None, None, None, 0.1, True, -1, 0, 0.0,
+                           True, 0)
+    assert o.dtype == torch.bfloat16
+    o, _ = ops.fwd(q8, k8, k8, None, 0.0, 0.1, True, -1, 0, 0.0)
+    assert o.dtype == torch.bfloat16
 
 
 def test_no_cpu_fallback():
