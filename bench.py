@@ -293,34 +293,122 @@ def time_case(c, hip, torch, steps, warmup):
             "combine_us": mean([s[2] for s in st]) * 1e3}
 
 
-def cpu_baseline(c, torch):
-    """The oracle (C restatement of the reference golden) on the host cores, on
-    a bounded sample of config 2: the first `nb` sequences, all heads."""
-    import numpy as np
-    from oracle import fa_oracle as orc
-    nthreads = min(16, os.cpu_count() or 1)
-    B = c["B"]
-    q, kn, vn, caches = c["keep"][0], c["keep"][1], c["keep"][2], c["keep"][3]
-    kc, vc = caches[0]
-    L = c["L"]
-    nb = min(B, 8)
-    bits = lambda t: t[:nb].contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
-    qh, kh, vh, knh, vnh = bits(q), bits(kc), bits(vc), bits(kn), bits(vn)
+CPU_BUDGET_S = 10.0   # wall time per config for the CPU golden
+
+
+def _cpu_threads():
+    return min(16, os.cpu_count() or 1)
+
+
+def _timed(fn):
+    """Runs fn until CPU_BUDGET_S has passed (at least once);
+    returns (seconds per run, runs)."""
     t0 = time.perf_counter()
     reps = 0
     while True:
-        orc.kvcache_forward(qh, kh, vh, dtype=orc.BF16, cache_seqlens=L[:nb].numpy(), k=knh, v=vnh, causal=True,
-                            nthreads=nthreads)
+        fn()
         reps += 1
-        if time.perf_counter() - t0 > 10.0 or reps >= 20:
+        if time.perf_counter() - t0 > CPU_BUDGET_S or reps >= 1000:
             break
-    dt = (time.perf_counter() - t0) / reps
-    Hk, D = c["Hk"], 128
-    Ls = L[:nb]
-    sample_bytes = 2 * int((Ls + 1).sum()) * Hk * D * 2 + 2 * nb * c["H"] * D * 2 + 4 * nb * c["H"] + 2 * 2 * nb * Hk * D * 2
-    return {"value": sample_bytes / dt / 1e12, "unit": "TB/s", "cores": nthreads, "kind": "port",
-            "sample": f"config 2, sequences 0..{nb - 1} of {B} (all 32 q heads), oracle/fa_oracle.c with "
-                      f"{nthreads} OpenMP threads, {reps} reps, {dt * 1e3:.1f} ms/rep"}
+    return (time.perf_counter() - t0) / reps, reps
+
+
+def cpu_baseline(c, torch):
+    """The oracle (the C restatement of the reference golden,
+    tests/test_flash_attn_npu_v3.py:87-146 of the reference) on the host cores,
+    on a bounded sample of the config's own inputs, in the config's unit:
+      c2 / c3: the first sequences (all heads), TB/s of the same algorithmic bytes;
+      c4: one (batch, kv head) slice (its 4 query heads, rotary and append), TFLOP/s;
+      c5: the whole config, TB/s."""
+    import numpy as np
+    from oracle import fa_oracle as orc
+    nt = _cpu_threads()
+    name = c["name"]
+    q, kn, vn, caches, bt, bidx, cos, sin, alibi = c["keep"][:9]
+    kc, vc = caches[0]
+    L = c["L"]
+    H, Hk, D = c["H"], c["Hk"], 128
+    bits = lambda t: t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+    if name in ("c2", "c3"):
+        nb = 8 if name == "c2" else 4
+        qh, knh, vnh = bits(q[:nb]), bits(kn[:nb]), bits(vn[:nb])
+        if bt is None:
+            kh, vh, bth = bits(kc[:nb]), bits(vc[:nb]), None
+        else:  # the pages the sample's sequences use, renumbered
+            rows = bt[:nb].cpu()
+            used = torch.unique(rows)
+            remap = torch.zeros(int(used.max()) + 1, dtype=torch.int32)
+            remap[used.long()] = torch.arange(used.numel(), dtype=torch.int32)
+            kh, vh = bits(kc[used.to(kc.device).long()]), bits(vc[used.to(vc.device).long()])
+            bth = remap[rows.long()].numpy()
+        Ls = L[:nb]
+        dt, reps = _timed(lambda: orc.kvcache_forward(qh, kh, vh, dtype=orc.BF16, cache_seqlens=Ls.numpy(), k=knh,
+                                                      v=vnh, block_table=bth, causal=True, nthreads=nt))
+        nbytes = 2 * int((Ls + 1).sum()) * Hk * D * 2 + 2 * nb * H * D * 2 + 4 * nb * H + 2 * 2 * nb * Hk * D * 2
+        return {"value": round(nbytes / dt / 1e12, 6), "unit": "TB/s", "cores": nt, "host_cores": os.cpu_count(),
+                "kind": "port", "sample": f"config {name[1]}, sequences 0..{nb - 1} of {c['B']} (all {H} q heads), "
+                f"oracle/fa_oracle.c on {nt} OpenMP threads, {reps} reps, {dt * 1e3:.1f} ms/rep"}
+    if name == "c4":
+        g = H // Hk
+        qh = bits(q[0:1, :, 0:g])
+        kh, vh = bits(kc[0:1, :, 0:1]), bits(vc[0:1, :, 0:1])
+        knh, vnh = bits(kn[0:1, :, 0:1]), bits(vn[0:1, :, 0:1])
+        ch, sh = bits(cos), bits(sin)
+        dt, reps = _timed(lambda: orc.kvcache_forward(qh, kh, vh, dtype=orc.BF16, cache_seqlens=L[0:1].numpy(), k=knh,
+                                                      v=vnh, rotary_cos=ch, rotary_sin=sh, rotary_interleaved=False,
+                                                      causal=True, nthreads=nt))
+        flops = c["flops"] / (c["B"] * H) * g
+        return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": nt, "host_cores": os.cpu_count(),
+                "kind": "port", "sample": f"config 4, batch 0 x kv head 0 (q heads 0..{g - 1}): 1/{c['B'] * Hk} of "
+                f"the work, oracle/fa_oracle.c on {nt} OpenMP threads, {reps} reps, {dt * 1e3:.0f} ms/rep"}
+    # c5: the whole config
+    qh, kh, vh = bits(q), bits(kc), bits(vc)
+    dt, reps = _timed(lambda: orc.kvcache_forward(qh, kh, vh, dtype=orc.BF16, cache_seqlens=L.numpy(),
+                                                  cache_batch_idx=bidx.cpu().numpy(), block_table=bt.cpu().numpy(),
+                                                  causal=True, window=(4096, 0), alibi=alibi.cpu().numpy(),
+                                                  nthreads=nt))
+    return {"value": round(c["attn_bytes"] / dt / 1e12, 6), "unit": "TB/s", "cores": nt,
+            "host_cores": os.cpu_count(), "kind": "port",
+            "sample": f"config 5, all {c['B']} sequences, oracle/fa_oracle.c on {nt} OpenMP threads, {reps} reps, "
+                      f"{dt * 1e3:.1f} ms/rep"}
+
+
+def ceilings(torch, hip):
+    """Practical ceilings of this part, measured with library kernels: HBM
+    bandwidth of a 4 GiB device copy (read + write) and of a 4 GiB reduction
+    (read), and bf16 TFLOP/s of a large GEMM (torch.matmul, hipBLASLt)."""
+    stream = torch.cuda.current_stream().cuda_stream
+    res = {}
+
+    def timed(fn, n):
+        fn()
+        torch.cuda.synchronize()
+        a, b = hip.event(), hip.event()
+        hip.record(a, stream)
+        for _ in range(n):
+            fn()
+        hip.record(b, stream)
+        return hip.ms(a, b) / n * 1e-3
+
+    x = torch.empty(1 << 31, dtype=torch.bfloat16, device="cuda").normal_()
+    y = torch.empty_like(x)
+    t = timed(lambda: y.copy_(x), 10)
+    res["hbm_copy_tbps"] = round(2 * x.numel() * 2 / t / 1e12, 3)
+    acc = torch.empty((), dtype=torch.float32, device="cuda")
+    t = timed(lambda: torch.sum(x, dim=0, dtype=torch.float32, out=acc), 10)
+    res["hbm_read_tbps"] = round(x.numel() * 2 / t / 1e12, 3)
+    del x, y
+    n = 8192
+    a = torch.randn((n, n), device="cuda").to(torch.bfloat16)
+    b = torch.randn((n, n), device="cuda").to(torch.bfloat16)
+    c = torch.empty((n, n), device="cuda", dtype=torch.bfloat16)
+    for _ in range(20):
+        torch.matmul(a, b, out=c)  # clock warm-up
+    t = timed(lambda: torch.matmul(a, b, out=c), 50)
+    res["gemm_bf16_tflops"] = round(2 * n ** 3 / t / 1e12, 1)
+    res["note"] = "4 GiB bf16 copy (2 x 4 GiB moved), torch.sum of 4 GiB bf16, 8192^3 bf16 torch.matmul"
+    torch.cuda.empty_cache()
+    return res
 
 
 def bench_bwd(torch, hip, steps, warmup):
@@ -371,11 +459,11 @@ def bench_bwd(torch, hip, steps, warmup):
             "workload": f"backward, dense causal B{B} S{S} H{H}/{Hk} D{D} bf16 (dsum + dK/dV + dQ kernels)"}
 
 
-TRAFFIC_PROFILE = "profiles/fa_decode_kernel_hbm_traffic.txt"
+TRAFFIC_PROFILE = "profiles/fa_attention_kernels_hbm_traffic.txt"
 
 
 def measured_traffic(cfg):
-    """HBM bytes per launch of the decode kernel on `cfg`, as measured by the two
+    """HBM bytes per launch of the attention kernel on `cfg`, as measured by the two
     rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) summarised in TRAFFIC_PROFILE
     (scaled by the plain-copy calibration recorded there); None if absent."""
     import re
@@ -393,6 +481,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="c2,c3,c4,c5,bwd,c2f8,c3f8")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="also measure this part's practical HBM and bf16 GEMM ceilings with library kernels")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 plain device copies of 1 GiB (reference for rocprof FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -410,7 +500,6 @@ def main():
     if "c2" not in names:
         names = ["c2"] + names
     results = {}
-    cases = {}
     for name in names:
         if name == "bwd":
             r = bench_bwd(torch, hip, args.steps, args.warmup)
@@ -431,19 +520,26 @@ def main():
             r["attn_bytes"] = c["attn_bytes"]
             r["attn_tbps"] = c["attn_bytes"] / (t["attn_us"] * 1e-6) / 1e12
             r["attn_frac_hbm"] = r["attn_tbps"] * 1e3 / HBM_PEAK_GBS
+            r["roofline"] = {"bound": "hbm", "achieved": round(r["attn_tbps"] * 1e3, 1), "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": round(r["attn_frac_hbm"], 4),
+                             "traffic": measured_traffic(name), "kernel": "fa_decode_kernel",
+                             "kernel_us": round(t["attn_us"], 2), "algorithmic_bytes": c["attn_bytes"]}
         else:
             r["flops_per_call"] = c["flops"]
             r["tflops_call"] = c["flops"] / (t["us_per_call"] * 1e-6) / 1e12
             r["attn_tflops"] = c["flops"] / (t["attn_us"] * 1e-6) / 1e12
             r["attn_frac_mfma"] = r["attn_tflops"] / BF16_PEAK_TFLOPS
+            r["roofline"] = {"bound": "mfma", "achieved": round(r["attn_tflops"], 1), "peak": BF16_PEAK_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(r["attn_frac_mfma"], 4), "traffic": measured_traffic(name),
+                             "kernel": "fa_prefill_kernel", "kernel_us": round(t["attn_us"], 2),
+                             "algorithmic_flops": c["flops"]}
+        if not args.no_cpu and name in ("c2", "c3", "c4", "c5"):
+            r["cpu_baseline"] = cpu_baseline(c, torch)
         results[name] = r
         print(f"# {name}: {json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})}",
               file=sys.stderr, flush=True)
-        if name == "c2":
-            cases["c2"] = c
-        else:
-            del c
-            torch.cuda.empty_cache()
+        del c
+        torch.cuda.empty_cache()
 
     if args.copy_calibration:
         src = torch.ones(1 << 28, dtype=torch.int32, device=dev)  # 1 GiB read, 1 GiB written
@@ -454,9 +550,10 @@ def main():
         del src, dst
     c2 = results["c2"]
     traffic = measured_traffic("c2")
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(cases["c2"], torch)
+    cpu = c2.get("cpu_baseline")
+    if args.ceilings:
+        results["ceilings"] = ceilings(torch, hip)
+        print(f"# ceilings: {json.dumps(results['ceilings'])}", file=sys.stderr, flush=True)
     line = {
         "metric": METRIC,
         "value": round(c2["tbps_call"], 4),
@@ -481,6 +578,7 @@ def main():
         "cpu_baseline": cpu,
         "configs": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in results.items()},
+        "host_cores": os.cpu_count(),
     }
     print(json.dumps(line))
 
