@@ -474,6 +474,95 @@ def measured_traffic(cfg):
     return int(m.group(1)) if m else None
 
 
+PHASES_LIB = os.path.join(REPO, "flash-attention-npu_amd", "fa_mi355x", "lib", "libfa_mi355x_phases.so")
+
+
+def decode_phases(names, torch, hip, reps):
+    """Phase breakdown of the decode kernel from the per-wave real-time stamps
+    (100 MHz) of the instrumented library (build.py: FA_DECODE_PHASES), in µs,
+    medians over `reps` calls:
+      plan        entry -> end of the in-LDS plan (median wave)
+      first_tile  end of the plan -> end of the wave's first tile (median wave)
+      start       kernel start -> median first-tile end (plan + pipeline fill)
+      steady      median first-tile end -> median wave exit
+      tail        median wave exit -> last wave exit
+      kernel      first wave entry -> last wave exit
+      merge       the merge kernel (stage events around it)
+    plus the median exit per XCD and per segment count."""
+    import numpy as np
+    from fa_mi355x import capi
+    L = ctypes.CDLL(PHASES_LIB, mode=os.RTLD_LOCAL)
+    L.fa_mha_fwd_kvcache.argtypes = [ctypes.POINTER(capi.FwdParams), ctypes.c_void_p]
+    L.fa_decode_phase_stamps.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int)]
+    hip.lib.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.lib.hipMemset.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t]
+    stream = torch.cuda.current_stream().cuda_stream
+    workers = torch.cuda.get_device_properties(0).multi_processor_count * 4
+    out = {}
+    for name in names:
+        ncopy = {"c2": 2, "c3": 2, "c5": 4, "c2f8": 2, "c3f8": 2}[name]
+        c = build_case(name, torch, "cuda", ncopy)
+        ps = c["params"]
+        buf, cap = ctypes.c_void_p(), ctypes.c_int()
+        assert L.fa_decode_phase_stamps(ctypes.byref(buf), ctypes.byref(cap)) == 0
+        assert workers <= cap.value
+        for i in range(20):
+            assert L.fa_mha_fwd_kvcache(ctypes.byref(ps[i % len(ps)]), stream) == 0
+        torch.cuda.synchronize()
+        runs = []
+        for rep in range(reps):
+            assert hip.lib.hipMemset(buf, 0, cap.value * 64) == 0
+            p = ps[rep % len(ps)]
+            evs = [hip.event() for _ in range(4)]
+            arr = (ctypes.c_void_p * 4)(*[e.value for e in evs])
+            p.stage_events = ctypes.cast(arr, ctypes.c_void_p)
+            assert L.fa_mha_fwd_kvcache(ctypes.byref(p), stream) == 0
+            p.stage_events = None
+            torch.cuda.synchronize()
+            merge_us = hip.ms(evs[2], evs[3]) * 1e3
+            raw = np.zeros(cap.value * 8, dtype=np.uint64)
+            assert hip.lib.hipMemcpy(raw.ctypes.data, buf, raw.nbytes, 2) == 0
+            s = raw.reshape(cap.value, 8)[:workers].astype(np.int64)
+            live = s[:, 5] > 0
+            k0 = s[:, 0].min()
+            us = lambda col: (col - k0) / 100.0  # 100 MHz ticks -> µs
+            entry, plan, first, exit_ = us(s[:, 0]), us(s[:, 1]), us(s[:, 2]), us(s[:, 3])
+            med_exit = float(np.median(exit_[live]))
+            med_first = float(np.median(first[live]))
+            xcc = s[:, 7] & 0xF
+            r = {"plan": float(np.median(plan - entry)), "first_tile": float(np.median((first - plan)[live])),
+                 "start": med_first, "steady": med_exit - med_first, "tail": float(exit_.max()) - med_exit,
+                 "kernel": float(exit_.max()), "dispatch_spread": float(entry.max()),
+                 "exit_p10": float(np.percentile(exit_[live], 10)), "exit_p90": float(np.percentile(exit_[live], 90)),
+                 "merge": merge_us, "tiles_per_wave": float(s[live, 5].mean()),
+                 "segments_mean": float(s[live, 4].mean()), "segments_max": int(s[live, 4].max())}
+            # spread of the exits between CUs and within a CU (HW_ID: CU, SH, SE fields)
+            hw = s[:, 6]
+            cu = xcc * 1000 + ((hw >> 13) & 7) * 100 + ((hw >> 12) & 1) * 16 + ((hw >> 8) & 15)
+            ids = np.unique(cu[live])
+            means = np.array([exit_[live & (cu == u)].mean() for u in ids])
+            within = np.concatenate([exit_[live & (cu == u)] - exit_[live & (cu == u)].mean() for u in ids])
+            r["exit_sd_between_cu"] = float(means.std())
+            r["exit_sd_within_cu"] = float(within.std())
+            for x in range(8):
+                sel = live & (xcc == x)
+                r[f"exit_xcd{x}"] = float(np.median(exit_[sel])) if sel.any() else None
+            for n in sorted(set(s[live, 4].tolist()))[:8]:
+                sel = live & (s[:, 4] == n)
+                r[f"exit_nseg{n}"] = float(np.median(exit_[sel]))
+            runs.append(r)
+        med = {}
+        for k in runs[0]:
+            vals = [rr[k] for rr in runs if rr.get(k) is not None]
+            med[k] = round(float(np.median(vals)), 2) if vals else None
+        med["workload"] = c["work_desc"]
+        out[name] = med
+        print(f"# {name}: {json.dumps(med)}", file=sys.stderr, flush=True)
+        del c
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -485,6 +574,9 @@ def main():
                     help="also measure this part's practical HBM and bf16 GEMM ceilings with library kernels")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 plain device copies of 1 GiB (reference for rocprof FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--phases", action="store_true",
+                    help="instead of the bench line: the decode kernel's per-wave phase breakdown on the decode "
+                         "configs of --configs, from the instrumented library (libfa_mi355x_phases.so)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -497,6 +589,10 @@ def main():
     dev = "cuda"
     hip = Hip()
     names = [s.strip() for s in args.configs.split(",") if s.strip()]
+    if args.phases:
+        dec = [n for n in names if n in ("c2", "c3", "c5", "c2f8", "c3f8")]
+        print(json.dumps({"phases_us": decode_phases(dec, torch, hip, max(args.steps, 1))}))
+        return
     if "c2" not in names:
         names = ["c2"] + names
     results = {}

@@ -2,6 +2,9 @@
 
   fa_mi355x/lib/libfa_mi355x.so        HIP kernels for gfx950 + the C ABI (include/fa_mi355x.h)
   fa_mi355x/lib/libfa_mi355x_torch.so  torch.ops.fa_mi355x operators over that C ABI
+  fa_mi355x/lib/libfa_mi355x_phases.so the same C ABI with per-wave real-time
+                                       stamps in the decode kernel (FA_DECODE_PHASES),
+                                       read by bench.py --phases; never loaded otherwise
 
 Usage: python build.py [--jobs N]. hipcc cross-compiles for gfx950, so this
 runs on a machine without a GPU.
@@ -40,9 +43,9 @@ def _run(cmd):
     return out
 
 
-def _compile_hip(src):
-    obj = os.path.join(OBJDIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC] + HIPFLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+def _compile_hip(src, defines=(), tag=""):
+    obj = os.path.join(OBJDIR, os.path.basename(src) + tag + ".o")
+    cmd = [HIPCC] + HIPFLAGS + [f"-D{d}" for d in defines] + ["-c", os.path.join(CSRC, src), "-o", obj]
     _run(cmd)
     return obj
 
@@ -73,13 +76,21 @@ def build(jobs=8, verbose=True):
     torch_cmd = ["g++"] + cflags + ["-c", os.path.join(CSRC, "torch_ext", "fa_torch_ops.cpp"), "-o", torch_obj]
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         futs = [ex.submit(_compile_hip, s) for s in HIP_SOURCES]
+        pfut = ex.submit(_compile_hip, "fa_decode.hip", ("FA_DECODE_PHASES",), ".phases")
         tfut = ex.submit(_run, torch_cmd)
         objs = [f.result() for f in futs]
+        pobj = pfut.result()
         tfut.result()
     core = os.path.join(LIBDIR, "libfa_mi355x.so")
     tmp = core + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", tmp] + objs)
     os.replace(tmp, core)
+    phases = os.path.join(LIBDIR, "libfa_mi355x_phases.so")
+    pobjs = [pobj if os.path.basename(o) == "fa_decode.hip.o" else o for o in objs]
+    # -Bsymbolic: the instrumented library binds its own kernels even beside the product library
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-Wl,-Bsymbolic", "-o", phases + ".tmp"]
+         + pobjs)
+    os.replace(phases + ".tmp", phases)
     tlib = os.path.join(LIBDIR, "libfa_mi355x_torch.so")
     tmp = tlib + ".tmp"
     _run(["g++", "-shared", "-o", tmp, torch_obj, "-L", LIBDIR, "-lfa_mi355x", "-Wl,-rpath,$ORIGIN"] + ldflags)

@@ -31,6 +31,18 @@ constexpr int TABN = 256;    // paged: block ids staged per wave
 constexpr int MAXB = 2048;
 }  // namespace dec
 
+#ifdef FA_DECODE_PHASES
+// Instrumented build only (libfa_mi355x_phases.so, never the product
+// library): per-wave real-time stamps (s_memrealtime, 100 MHz) of the last
+// decode launch, 8 words per wave: entry, end of the plan, end of the first
+// tile, exit, segments, tiles, HW_ID, XCC_ID. bench.py --phases reads them.
+constexpr int kPhaseWaves = 8192;
+__device__ unsigned long long fa_phase_stamps[kPhaseWaves * 8];
+#define FA_PHASE(...) __VA_ARGS__
+#else
+#define FA_PHASE(...)
+#endif
+
 // Tile shape per kernel head dim and stored element size EB: a tile is 16 KB
 // of K and V (32 keys at head dim 128, 64 keys at 64), so a wave keeps the
 // same bytes in flight and every lane loads full 16-byte chunks. FP8 tiles
@@ -134,6 +146,17 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, G = lane >> 4;
+    FA_PHASE(const unsigned long long ph_entry = __builtin_amdgcn_s_memrealtime();
+             unsigned long long ph_plan = 0, ph_first = 0, ph_nseg = 0;
+             auto ph_write = [&](long long w, long long ntiles) {
+                 if (lane == 0 && w < kPhaseWaves) {
+                     unsigned long long* o = fa_phase_stamps + w * 8;
+                     o[0] = ph_entry; o[1] = ph_plan; o[2] = ph_first;
+                     o[3] = __builtin_amdgcn_s_memrealtime(); o[4] = ph_nseg; o[5] = (unsigned long long)ntiles;
+                     o[6] = (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 4);   // HW_ID
+                     o[7] = (unsigned)__builtin_amdgcn_s_getreg((15 << 11) | 20);  // XCC_ID
+                 }
+             };)
 
     // ---- plan: tiles per segment, prefix over batches -------------------------------
     for (int b = tid; b < a.B; b += 256) {
@@ -171,6 +194,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     const long long W = (long long)gridDim.x * NWAVE;
     const long long wid = (long long)blockIdx.x * NWAVE + wave;
     const int t0 = (int)(wid * T / W), t1 = (int)((wid + 1) * T / W);
+    FA_PHASE(ph_plan = __builtin_amdgcn_s_memrealtime(); if (t0 >= t1) ph_write(wid, 0);)
     if (t0 >= t1) return;  // no block barrier follows: waves are independent from here
 
     const ET* qp = static_cast<const ET*>(a.q);
@@ -514,12 +538,15 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                     end_seg(cs);
                     cs = dec_seg_of(a, s_pref, s_bat, t);
                     begin_seg(cs);
+                    FA_PHASE(++ph_nseg;)
                 }
                 compute(t, kr[st], vr[st], bk[st]);
+                FA_PHASE(if (t == t0) ph_first = __builtin_amdgcn_s_memrealtime();)
             }
         }
     }
     end_seg(cs);
+    FA_PHASE(++ph_nseg; ph_write(wid, t1 - t0);)
 }
 
 // Merge of the partials a segment left in the decode kernel (4 workgroups per
@@ -707,3 +734,11 @@ hipError_t launch_decode_merge(const FwdArgs& a, int dtype, int d, int grid, hip
 }
 
 }  // namespace fa
+
+#ifdef FA_DECODE_PHASES
+// Device address and capacity (waves) of the stamp buffer of the instrumented build.
+extern "C" __attribute__((visibility("default"))) int fa_decode_phase_stamps(void** ptr, int* waves) {
+    *waves = fa::kPhaseWaves;
+    return (int)hipGetSymbolAddress(ptr, HIP_SYMBOL(fa::fa_phase_stamps));
+}
+#endif
