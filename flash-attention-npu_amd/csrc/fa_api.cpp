@@ -82,6 +82,7 @@ struct Plan {
     bool decode;
     int BM, BN;
     int g;
+    int hk_eff;         // heads that own row tiles: nheads_k, or nheads without GQA packing
     int rows_max;       // packed rows per (b, kv head) bound
     int mt_max;
     int kv_capacity;
@@ -123,6 +124,17 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
     FA_CHECK(p->nheads >= 1 && p->nheads_k >= 1, "number of heads must be positive");
     FA_CHECK(p->nheads % p->nheads_k == 0, "Number of heads in key/value must divide number of heads in query");
     FA_CHECK(p->headdim >= 1, "head dimension must be positive");
+    if (p->qv) {
+        FA_CHECK(!f8, "qv is not supported with FP8 inputs");
+        FA_CHECK(aligned16(p->qv) && strides8(p->qv_batch_stride, p->qv_row_stride, p->qv_head_stride),
+                 "qv must be 16-byte aligned with strides that are multiples of 8 elements");
+        const int64_t rows = (int64_t)p->seqlen_q * (p->no_pack_gqa ? 1 : p->nheads / p->nheads_k);
+        if (rows > kDecodeRows || p->headdim > 128)
+            return fail(FA_EUNSUPPORTED,
+                        "qv is supported where the decode kernel runs: at most %d query rows per kv head "
+                        "(seqlen_q * nheads / nheads_k) and headdim <= 128",
+                        kDecodeRows);
+    }
     FA_CHECK(p->headdim % 8 == 0, "head dimension must be a multiple of 8");
     FA_CHECK(p->headdim <= 256, "FlashAttention only supports head dimension at most 256");
     FA_CHECK(p->headdim_v == p->headdim, "headdim_v (%d) must equal headdim (%d)", p->headdim_v, p->headdim);
@@ -211,7 +223,8 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
 }
 
 void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
-    pl.g = p->nheads / p->nheads_k;
+    pl.hk_eff = p->no_pack_gqa ? p->nheads : p->nheads_k;
+    pl.g = p->nheads / pl.hk_eff;
     pl.rows_max = p->seqlen_q * pl.g;
     // kernel head dim: the prefill kernels come at 64, 128 and 256, the
     // decode kernel at 64 and 128; each serves the head dims up to its own
@@ -249,7 +262,7 @@ void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
         pl.min_chunk = 0;
     } else {
         const int occ = 2;  // prefill workgroups per CU
-        const int64_t base_bound = (int64_t)pb * p->nheads_k * pl.mt_max;
+        const int64_t base_bound = (int64_t)pb * pl.hk_eff * pl.mt_max;
         pl.workers = 0;
         pl.target_items = 2 * cus;
         pl.min_chunk = 2 * pl.BN;
@@ -327,7 +340,8 @@ fa_status_t run_forward_ws(const fa_fwd_params* p, int kind, void* stream_v, voi
     // append, as does a batch run in chunks.
     const bool local_left = p->window_size_left >= 0 || p->attention_chunk > 0;
     const bool fused_append = kind == FA_KIND_KVCACHE && p->k_new && pl.decode && !pl.rotary && !p->cu_seqlens_k_new &&
-                              !p->cu_seqlens_q && !chunked && (p->seqlen_new <= p->seqlen_q || !local_left);
+                              !p->cu_seqlens_q && !chunked && !p->no_pack_gqa &&
+                              (p->seqlen_new <= p->seqlen_q || !local_left);
     if (kind == FA_KIND_KVCACHE && p->k_new && !fused_append) {
         fa::KvPrepArgs k{};
         k.k_new = p->k_new;
@@ -447,8 +461,13 @@ fa_status_t run_forward_ws(const fa_fwd_params* p, int kind, void* stream_v, voi
         a.Sq = p->seqlen_q;
         a.Sk = kind == FA_KIND_KVCACHE ? pl.kv_capacity : p->seqlen_k;
         a.H = p->nheads;
-        a.Hk = p->nheads_k;
+        a.Hk = pl.hk_eff;
         a.g = pl.g;
+        a.kvdiv = pl.hk_eff / p->nheads_k;
+        a.qv = ragged_q || !p->qv ? p->qv : boff(p->qv, b0, p->qv_batch_stride, 2);
+        a.qv_sb = p->qv_batch_stride;
+        a.qv_si = p->qv_row_stride;
+        a.qv_sh = p->qv_head_stride;
         a.hd = p->headdim;
         a.seqlen_new = (kind == FA_KIND_KVCACHE && p->k_new && !p->cu_seqlens_k_new) ? p->seqlen_new : 0;
         if (kind == FA_KIND_KVCACHE) {

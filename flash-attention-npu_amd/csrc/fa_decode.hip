@@ -236,10 +236,11 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                 b2 = min(max(a.block_table[(int64_t)s.crow * a.bt_stride + pidx], 0), a.num_blocks - 1);
             }
             const int inpage = a.page_shift >= 0 ? (key & (a.page - 1)) : key % a.page;
-            return base + (int64_t)b2 * sb + (int64_t)inpage * si + (int64_t)s.hk * sh;
+            return base + (int64_t)b2 * sb + (int64_t)inpage * si + (int64_t)(s.hk / a.kvdiv) * sh;
         }
-        if (LAYOUT == 2 && a.cu_seqlens_k) return base + ((int64_t)a.cu_seqlens_k[s.b] + key) * si + (int64_t)s.hk * sh;
-        return base + (int64_t)s.crow * sb + (int64_t)(s.lp + key) * si + (int64_t)s.hk * sh;
+        if (LAYOUT == 2 && a.cu_seqlens_k)
+            return base + ((int64_t)a.cu_seqlens_k[s.b] + key) * si + (int64_t)(s.hk / a.kvdiv) * sh;
+        return base + (int64_t)s.crow * sb + (int64_t)(s.lp + key) * si + (int64_t)(s.hk / a.kvdiv) * sh;
     };
 
     // With a fused append, keys nf .. sk - 1 come from k_new / v_new; the
@@ -272,8 +273,9 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                 const ET* vpr;
                 if (key >= first_new) {
                     const int tn = key - first_new;
-                    kpr = knp + (int64_t)is.b * a.kn_sb + (int64_t)tn * a.kn_si + (int64_t)is.hk * a.kn_sh + G * (D / 4);
-                    vpr = vnp + (int64_t)is.b * a.vn_sb + (int64_t)tn * a.vn_si + (int64_t)is.hk * a.vn_sh + G * (D / 4);
+                    const int64_t kvh = is.hk / a.kvdiv;
+                    kpr = knp + (int64_t)is.b * a.kn_sb + (int64_t)tn * a.kn_si + kvh * a.kn_sh + G * (D / 4);
+                    vpr = vnp + (int64_t)is.b * a.vn_sb + (int64_t)tn * a.vn_si + kvh * a.vn_sh + G * (D / 4);
                 } else {
                     kpr = row_ptr(kp, a.k_sb, a.k_si, a.k_sh, is, key, blk) + G * (D / 4);
                     vpr = row_ptr(vp, a.v_sb, a.v_si, a.v_sh, is, key, blk) + G * (D / 4);
@@ -297,6 +299,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     // ---- compute side --------------------------------------------------------------------
     DecSeg cs = dec_seg_of(a, s_pref, s_bat, t0);
     u32x4 qreg[KSTEPS];
+    u32x4 qvreg[KSTEPS];  // qv rows (16-bit inputs with qv only)
     u32x4 q8[2];  // FP8: the raw q bytes of dims G * D / 4 .. + D / 4 (zero-padded to 32)
     float slope = 0.f;
     int qi = 0;
@@ -331,12 +334,25 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                 const bool in = ok && (!HDM || (G * KSTEPS + s2) * 8 < a.hd);
                 qreg[s2] = in ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s2) * 8) : u32x4{0u, 0u, 0u, 0u};
             }
+            if (a.qv) {
+                // qv row of the same (position, head): B operand against V, as q against K
+                const ET* qvp = static_cast<const ET*>(a.qv);
+                const ET* qvrow = a.cu_seqlens_q
+                                      ? qvp + ((int64_t)a.cu_seqlens_q[s.b] + i) * a.qv_si + (int64_t)h * a.qv_sh
+                                      : qvp + (int64_t)s.b * a.qv_sb + (int64_t)i * a.qv_si + (int64_t)h * a.qv_sh;
+#pragma unroll
+                for (int s2 = 0; s2 < KSTEPS; ++s2) {
+                    const bool in = ok && (!HDM || (G * KSTEPS + s2) * 8 < a.hd);
+                    qvreg[s2] = in ? *reinterpret_cast<const u32x4*>(qvrow + (G * KSTEPS + s2) * 8) : u32x4{0u, 0u, 0u, 0u};
+                }
+            }
         }
         if constexpr (F8) {
-            const float qk = descale_at(a.qd, a.qd_sb, a.qd_sh, s.b, s.hk) * descale_at(a.kd, a.kd_sb, a.kd_sh, s.b, s.hk);
+            const int kvh = s.hk / a.kvdiv;
+            const float qk = descale_at(a.qd, a.qd_sb, a.qd_sh, s.b, kvh) * descale_at(a.kd, a.kd_sb, a.kd_sh, s.b, kvh);
             sc_qk = a.scale * qk;
             sc_qk2 = a.scale_log2 * qk;
-            sc_v = descale_at(a.vd, a.vd_sb, a.vd_sh, s.b, s.hk);
+            sc_v = descale_at(a.vd, a.vd_sb, a.vd_sh, s.b, kvh);
         }
         m_run = -INFINITY;
         l_run = 0.f;
@@ -437,6 +453,13 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
                 for (int h = 0; h < NH; ++h) sacc[h] = mfma16x16x32<DT>(opnd(kk, h, s), qreg[s], sacc[h]);
+            if (a.qv) {
+                // S^T += V . Qv^T: the V loads carry the same lane layout as the K loads
+#pragma unroll
+                for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+                    for (int h = 0; h < NH; ++h) sacc[h] = mfma16x16x32<DT>(opnd(vv, h, s), qvreg[s], sacc[h]);
+            }
         }
         // online softmax (log2 domain), row = li, keys key0 + 16h + 4G + e
         const int sk = cs.sk, diag0 = cs.sk - cs.sq;

@@ -164,16 +164,6 @@ __device__ void build_schedule(const FwdArgs& a, int* s_pref, long long* s_red, 
 }
 
 
-__device__ __forceinline__ const uint16_t* kv_row_ptr(const FwdArgs& a, const uint16_t* base, int64_t sb,
-                                                      int64_t si, int64_t sh, int b, int crow, int j, int hk) {
-    if (a.block_table) {
-        int blk = a.block_table[(int64_t)crow * a.bt_stride + j / a.page];
-        blk = min(max(blk, 0), a.num_blocks - 1);
-        return base + (int64_t)blk * sb + (int64_t)(j % a.page) * si + (int64_t)hk * sh;
-    }
-    if (a.cu_seqlens_k) return base + ((int64_t)a.cu_seqlens_k[b] + j) * si + (int64_t)hk * sh;
-    return base + (int64_t)crow * sb + (int64_t)j * si + (int64_t)hk * sh;
-}
 
 
 
@@ -302,13 +292,14 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
         RT kr[CPT], vr[CPT];
         // per-item row bases: token j of this kv head lives at base + j * si
         // (contiguous / varlen) or at base + blk * sb + (j % page) * si (paged)
-        const ET* kb0 = kp + (int64_t)hk * a.k_sh + dch * 8;
-        const ET* vb0 = vp + (int64_t)hk * a.v_sh + dch * 8;
+        const int kvh = hk / a.kvdiv;  // kv head of this row tile's query heads
+        const ET* kb0 = kp + (int64_t)kvh * a.k_sh + dch * 8;
+        const ET* vb0 = vp + (int64_t)kvh * a.v_sh + dch * 8;
         // FP8: scores scale by q_descale * k_descale, the output by v_descale
         float sc_qk = a.scale, sc_v = 1.f;
         if constexpr (F8) {
-            sc_qk = a.scale * descale_at(a.qd, a.qd_sb, a.qd_sh, b, hk) * descale_at(a.kd, a.kd_sb, a.kd_sh, b, hk);
-            sc_v = descale_at(a.vd, a.vd_sb, a.vd_sh, b, hk);
+            sc_qk = a.scale * descale_at(a.qd, a.qd_sb, a.qd_sh, b, kvh) * descale_at(a.kd, a.kd_sb, a.kd_sh, b, kvh);
+            sc_v = descale_at(a.vd, a.vd_sb, a.vd_sh, b, kvh);
         }
         const int* btrow = nullptr;
         if constexpr (PAGED) {

@@ -80,6 +80,13 @@ struct FwdArgs {
     const float* kd;
     const float* vd;
     int64_t qd_sb, qd_sh, kd_sb, kd_sh, vd_sb, vd_sh;
+    // decode: scores += qv . v (qv like q with the head dim of v), null = off
+    const void* qv;
+    int64_t qv_sb, qv_si, qv_sh;
+    // the kv head of row-tile head hk is hk / kvdiv: 1 when the g query heads
+    // of a kv head share its row tiles (Hk, g as given), g when each query
+    // head has its own (Hk = H, g = 1)
+    int kvdiv;
 };
 
 // Backward (dense / varlen). Row layouts as in FwdArgs; lse and dsum share

@@ -131,7 +131,7 @@ std::tuple<Tensor, Tensor> kvcache_impl(const Tensor& q, Tensor& kcache, Tensor&
                                         int64_t window_size_left, int64_t window_size_right, int64_t attention_chunk,
                                         double softcap, bool is_rotary_interleaved, int64_t num_splits,
                                         const OptT& q_descale, const OptT& k_descale, const OptT& v_descale,
-                                        const OptT& workspace) {
+                                        const OptT& workspace, const OptT& qv, std::optional<bool> pack_gqa) {
     c10::DeviceGuard guard(q.device());
     TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
     check_dev(kcache, q, "k_cache");
@@ -267,6 +267,26 @@ std::tuple<Tensor, Tensor> kvcache_impl(const Tensor& q, Tensor& kcache, Tensor&
     p.attention_chunk = (int32_t)attention_chunk;
     p.num_splits = (int32_t)num_splits;
     set_descale(p, q_descale, k_descale, v_descale, q, batch);
+    Tensor qvc;
+    if (qv.has_value()) {
+        check_dev(*qv, q, "qv");
+        TORCH_CHECK(qv->scalar_type() == q.scalar_type(), "qv must have the same dtype as query");
+        TORCH_CHECK(qv->dim() == q.dim() && qv->size(0) == q.size(0) && qv->size(-2) == q.size(-2) &&
+                        (ragged_q || qv->size(1) == q.size(1)) && qv->size(-1) == p.headdim_v,
+                    "qv must have shape (batch_size, seqlen_q, num_heads, head_size_v), or (total_q, num_heads, "
+                    "head_size_v) with cu_seqlens_q");
+        qvc = qv->stride(-1) == 1 ? *qv : qv->contiguous();
+        p.qv = qvc.data_ptr();
+        if (ragged_q) {
+            p.qv_row_stride = qvc.stride(0);
+            p.qv_head_stride = qvc.stride(1);
+        } else {
+            p.qv_batch_stride = qvc.stride(0);
+            p.qv_row_stride = qvc.stride(1);
+            p.qv_head_stride = qvc.stride(2);
+        }
+    }
+    p.no_pack_gqa = pack_gqa.has_value() && !*pack_gqa ? 1 : 0;
     Tensor out = at::empty(q.sizes(), out_options(q));
     Tensor lse = ragged_q ? at::empty({q.size(1), q.size(0)}, q.options().dtype(at::kFloat))
                           : at::empty({q.size(0), q.size(2), q.size(1)}, q.options().dtype(at::kFloat));
@@ -295,7 +315,8 @@ std::tuple<Tensor, Tensor> fwd_kvcache(const Tensor& q, Tensor& kcache, Tensor& 
     return kvcache_impl(q, kcache, vcache, k_new, v_new, seqlens_k, rotary_cos, rotary_sin, cache_batch_idx,
                         leftpad_k, block_table, alibi_slopes, std::nullopt, std::nullopt, 0, std::nullopt,
                         softmax_scale, is_causal, window_size_left, window_size_right, 0, softcap,
-                        is_rotary_interleaved, num_splits, std::nullopt, std::nullopt, std::nullopt, std::nullopt);
+                        is_rotary_interleaved, num_splits, std::nullopt, std::nullopt, std::nullopt, std::nullopt,
+                        std::nullopt, std::nullopt);
 }
 
 std::tuple<Tensor, Tensor> fwd_kvcache_v3(const Tensor& q, Tensor& kcache, Tensor& vcache, const OptT& k_new,
@@ -308,12 +329,13 @@ std::tuple<Tensor, Tensor> fwd_kvcache_v3(const Tensor& q, Tensor& kcache, Tenso
                                           int64_t window_size_left, int64_t window_size_right,
                                           int64_t attention_chunk, double softcap, bool is_rotary_interleaved,
                                           int64_t num_splits, const OptT& q_descale, const OptT& k_descale,
-                                          const OptT& v_descale, const OptT& workspace) {
+                                          const OptT& v_descale, const OptT& workspace, const OptT& qv,
+                                          std::optional<bool> pack_gqa) {
     return kvcache_impl(q, kcache, vcache, k_new, v_new, seqlens_k, rotary_cos, rotary_sin, cache_batch_idx,
                         leftpad_k, block_table, alibi_slopes, cu_seqlens_q, cu_seqlens_k_new, max_seqlen_q,
                         rotary_seqlens, softmax_scale, is_causal, window_size_left, window_size_right,
                         attention_chunk, softcap, is_rotary_interleaved, num_splits, q_descale, k_descale,
-                        v_descale, workspace);
+                        v_descale, workspace, qv, pack_gqa);
 }
 
 // ---- flash_attn_func ------------------------------------------------------------------------
@@ -321,7 +343,7 @@ std::tuple<Tensor, Tensor> fwd(const Tensor& q, const Tensor& k, const Tensor& v
                                double p_dropout, double softmax_scale, bool is_causal, int64_t window_size_left,
                                int64_t window_size_right, double softcap, int64_t attention_chunk,
                                const OptT& q_descale, const OptT& k_descale, const OptT& v_descale,
-                               int64_t num_splits, const OptT& workspace) {
+                               int64_t num_splits, const OptT& workspace, std::optional<bool> pack_gqa) {
     c10::DeviceGuard guard(q.device());
     TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
     check_dev(k, q, "k");
@@ -373,6 +395,7 @@ std::tuple<Tensor, Tensor> fwd(const Tensor& q, const Tensor& k, const Tensor& v
     p.out_row_stride = out.stride(1);
     p.out_head_stride = out.stride(2);
     p.softmax_lse = lse.data_ptr<float>();
+    p.no_pack_gqa = pack_gqa.has_value() && !*pack_gqa ? 1 : 0;
     Tensor ws = attach_workspace(p, FA_KIND_DENSE, q, workspace);
     check_status(fa_mha_fwd(&p, cur_stream()));
     return {out, lse};
@@ -386,7 +409,7 @@ std::tuple<Tensor, Tensor> varlen_fwd(const Tensor& q, const Tensor& k, const Te
                                       double softmax_scale, bool is_causal, int64_t window_size_left,
                                       int64_t window_size_right, double softcap, int64_t attention_chunk,
                                       const OptT& q_descale, const OptT& k_descale, const OptT& v_descale,
-                                      int64_t num_splits, const OptT& workspace) {
+                                      int64_t num_splits, const OptT& workspace, std::optional<bool> pack_gqa) {
     c10::DeviceGuard guard(q.device());
     TORCH_CHECK(q.is_cuda(), "q must be on a GPU device");
     check_dev(k, q, "k");
@@ -463,6 +486,7 @@ std::tuple<Tensor, Tensor> varlen_fwd(const Tensor& q, const Tensor& k, const Te
     p.out_row_stride = out.stride(0);
     p.out_head_stride = out.stride(1);
     p.softmax_lse = lse.data_ptr<float>();
+    p.no_pack_gqa = pack_gqa.has_value() && !*pack_gqa ? 1 : 0;
     Tensor ws = attach_workspace(p, FA_KIND_VARLEN, q, workspace);
     check_status(fa_mha_varlen_fwd(&p, cur_stream()));
     return {out, lse};
@@ -689,21 +713,23 @@ TORCH_LIBRARY(fa_mi355x, m) {
     m.def(
         "fwd(Tensor q, Tensor k, Tensor v, Tensor? alibi_slopes, float p_dropout, float softmax_scale, bool is_causal, "
         "int window_size_left, int window_size_right, float softcap, int attention_chunk=0, Tensor? q_descale=None, "
-        "Tensor? k_descale=None, Tensor? v_descale=None, int num_splits=0, Tensor? workspace=None) -> (Tensor, Tensor)");
+        "Tensor? k_descale=None, Tensor? v_descale=None, int num_splits=0, Tensor? workspace=None, "
+        "bool? pack_gqa=None) -> (Tensor, Tensor)");
     m.def(
         "fwd_kvcache_v3(Tensor q, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor? k, Tensor? v, Tensor? seqlens_k, "
         "Tensor? rotary_cos, Tensor? rotary_sin, Tensor? cache_batch_idx, Tensor? leftpad_k, Tensor? block_table, "
         "Tensor? alibi_slopes, Tensor? cu_seqlens_q, Tensor? cu_seqlens_k_new, int max_seqlen_q, "
         "Tensor? rotary_seqlens, float softmax_scale, bool is_causal, int window_size_left, int window_size_right, "
         "int attention_chunk, float softcap, bool is_rotary_interleaved, int num_splits, Tensor? q_descale=None, "
-        "Tensor? k_descale=None, Tensor? v_descale=None, Tensor? workspace=None) -> (Tensor, Tensor)");
+        "Tensor? k_descale=None, Tensor? v_descale=None, Tensor? workspace=None, Tensor? qv=None, "
+        "bool? pack_gqa=None) -> (Tensor, Tensor)");
     m.def(
         "varlen_fwd(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor? cu_seqlens_k, Tensor? seqused_k, "
         "Tensor? block_table, "
         "Tensor? alibi_slopes, int max_seqlen_q, int max_seqlen_k, float p_dropout, float softmax_scale, "
         "bool is_causal, int window_size_left, int window_size_right, float softcap, int attention_chunk=0, "
         "Tensor? q_descale=None, Tensor? k_descale=None, Tensor? v_descale=None, int num_splits=0, "
-        "Tensor? workspace=None) -> (Tensor, Tensor)");
+        "Tensor? workspace=None, bool? pack_gqa=None) -> (Tensor, Tensor)");
     m.def("fwd_combine(Tensor out_partial, Tensor lse_partial, ScalarType? out_dtype) -> (Tensor, Tensor)");
     m.def("fwd_combine_out(Tensor out_partial, Tensor lse_partial, Tensor(a!) out) -> Tensor");
     m.def(

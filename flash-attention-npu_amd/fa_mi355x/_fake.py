@@ -25,7 +25,7 @@ def _fwd_kvcache_v3_fake(q, k_cache, v_cache, k, v, seqlens_k, rotary_cos, rotar
                          block_table, alibi_slopes, cu_seqlens_q, cu_seqlens_k_new, max_seqlen_q, rotary_seqlens,
                          softmax_scale, is_causal, window_size_left, window_size_right, attention_chunk, softcap,
                          is_rotary_interleaved, num_splits, q_descale=None, k_descale=None, v_descale=None,
-                         workspace=None):
+                         workspace=None, qv=None, pack_gqa=None):
     if cu_seqlens_q is not None:
         t, h, _ = q.shape
         return _out_like(q), q.new_empty((h, t), dtype=torch.float32)
@@ -36,7 +36,7 @@ def _fwd_kvcache_v3_fake(q, k_cache, v_cache, k, v, seqlens_k, rotary_cos, rotar
 @torch.library.register_fake("fa_mi355x::fwd")
 def _fwd_fake(q, k, v, alibi_slopes, p_dropout, softmax_scale, is_causal, window_size_left, window_size_right,
               softcap, attention_chunk=0, q_descale=None, k_descale=None, v_descale=None, num_splits=0,
-              workspace=None):
+              workspace=None, pack_gqa=None):
     b, sq, h, _ = q.shape
     return _out_like(q), q.new_empty((b, h, sq), dtype=torch.float32)
 
@@ -45,7 +45,7 @@ def _fwd_fake(q, k, v, alibi_slopes, p_dropout, softmax_scale, is_causal, window
 def _varlen_fwd_fake(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, block_table, alibi_slopes, max_seqlen_q, max_seqlen_k,
                      p_dropout, softmax_scale, is_causal, window_size_left, window_size_right, softcap,
                      attention_chunk=0, q_descale=None, k_descale=None, v_descale=None, num_splits=0,
-                     workspace=None):
+                     workspace=None, pack_gqa=None):
     t, h, _ = q.shape
     return _out_like(q), q.new_empty((h, t), dtype=torch.float32)
 

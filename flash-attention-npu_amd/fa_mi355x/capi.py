@@ -11,7 +11,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 CORE_LIB = os.path.join(_HERE, "lib", "libfa_mi355x.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 FA_OK, FA_EINVAL, FA_EUNSUPPORTED, FA_EHIP, FA_EWORKSPACE = 0, 1, 2, 3, 4
 FA_DTYPE_FP16, FA_DTYPE_BF16, FA_DTYPE_FP32, FA_DTYPE_FP8_E4M3 = 0, 1, 2, 3
 FA_KIND_KVCACHE, FA_KIND_DENSE, FA_KIND_VARLEN = 0, 1, 2
@@ -54,6 +54,8 @@ class FwdParams(ctypes.Structure):
         ("q_descale", _vp), ("q_descale_batch_stride", _i64), ("q_descale_head_stride", _i64),
         ("k_descale", _vp), ("k_descale_batch_stride", _i64), ("k_descale_head_stride", _i64),
         ("v_descale", _vp), ("v_descale_batch_stride", _i64), ("v_descale_head_stride", _i64),
+        ("qv", _vp), ("qv_batch_stride", _i64), ("qv_row_stride", _i64), ("qv_head_stride", _i64),
+        ("no_pack_gqa", _i32),
     ]
 
 

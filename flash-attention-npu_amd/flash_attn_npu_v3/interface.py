@@ -168,14 +168,34 @@ def _cu_from_lengths(lengths):
     return torch.cat([z, torch.cumsum(lengths, 0, dtype=torch.int32)])
 
 
+def _pack(pack_gqa):
+    return None if pack_gqa is None else bool(pack_gqa)
+
+
+def _qv_by_concat(attn, q, k, v, qv, return_lse):
+    """FlashAttention-3's qv for the prefill kernels: scores = q.k + qv.v is
+    one attention over the head dims of q and qv concatenated, against k and
+    v concatenated; v is zero-padded to that width and the padding sliced off
+    the output. (The decode kernel takes qv directly.)"""
+    if qv.dtype != q.dtype or qv.shape[:-1] != q.shape[:-1] or qv.shape[-1] != v.shape[-1]:
+        raise RuntimeError("qv must have the dtype of q and shape q.shape[:-1] + (headdim_v,)")
+    dv = v.shape[-1]
+    q2 = torch.cat([q, qv], dim=-1)
+    k2 = torch.cat([k, v], dim=-1)
+    v2 = torch.cat([v, torch.zeros_like(k)], dim=-1)
+    res = attn(q2, k2, v2)
+    if return_lse:
+        return res[0][..., :dv], res[1]
+    return res[..., :dv]
+
+
 class FlashAttnFunc(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, softmax_scale, causal, qv=None, q_descale=None, k_descale=None, v_descale=None,
                 window_size=(-1, -1), attention_chunk=0, softcap=0.0, num_splits=1, pack_gqa=None,
                 deterministic=False, sm_margin=0, return_softmax=False, scheduler_metadata=None):
-        _reject(qv=qv)
         if softmax_scale is None:
-            softmax_scale = q.shape[-1] ** (-0.5)
+            softmax_scale = (q.shape[-1] + (qv.shape[-1] if qv is not None else 0)) ** (-0.5)
         call = _describe(q.shape[0], q.shape[1], k.shape[1], q.shape[2], k.shape[2], q.shape[3], v.shape[3], q.dtype,
                          causal, window_size, attention_chunk, softcap, num_splits, 0, False)
         ws, md_splits = _metadata_for(scheduler_metadata, call, q.device)
@@ -184,7 +204,7 @@ class FlashAttnFunc(torch.autograd.Function):
         q, k, v = [maybe_contiguous(x) for x in (q, k, v)]
         out, softmax_lse = ops.fwd(q, k, v, None, 0.0, float(softmax_scale), bool(causal), int(window_size[0]),
                                    int(window_size[1]), float(softcap), int(attention_chunk), q_descale, k_descale,
-                                   v_descale, int(num_splits), ws)
+                                   v_descale, int(num_splits), ws, _pack(pack_gqa))
         if any(x.requires_grad for x in (q, k, v)):
             ctx.save_for_backward(q, k, v, out, softmax_lse)
             ctx.softmax_scale = softmax_scale
@@ -211,9 +231,9 @@ class FlashAttnVarlenFunc(torch.autograd.Function):
                 softmax_scale, causal, qv=None, q_descale=None, k_descale=None, v_descale=None, window_size=(-1, -1),
                 attention_chunk=0, softcap=0.0, num_splits=1, pack_gqa=None, deterministic=False, sm_margin=0,
                 return_softmax=False, scheduler_metadata=None):
-        _reject(seqused_q=seqused_q, qv=qv)
+        _reject(seqused_q=seqused_q)
         if softmax_scale is None:
-            softmax_scale = q.shape[-1] ** (-0.5)
+            softmax_scale = (q.shape[-1] + (qv.shape[-1] if qv is not None else 0)) ** (-0.5)
         call = _describe(cu_seqlens_q.numel() - 1, max_seqlen_q, max_seqlen_k, q.shape[1], k.shape[1], q.shape[2],
                          v.shape[2], q.dtype, causal, window_size, attention_chunk, softcap, num_splits, 0, True)
         ws, md_splits = _metadata_for(scheduler_metadata, call, q.device)
@@ -223,7 +243,8 @@ class FlashAttnVarlenFunc(torch.autograd.Function):
         out, softmax_lse = ops.varlen_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, None, None,
                                           int(max_seqlen_q), int(max_seqlen_k), 0.0, float(softmax_scale),
                                           bool(causal), int(window_size[0]), int(window_size[1]), float(softcap),
-                                          int(attention_chunk), q_descale, k_descale, v_descale, int(num_splits), ws)
+                                          int(attention_chunk), q_descale, k_descale, v_descale, int(num_splits), ws,
+                                          _pack(pack_gqa))
         if any(x.requires_grad for x in (q, k, v)):
             ctx.save_for_backward(q, k, v, out, softmax_lse, cu_seqlens_q, cu_seqlens_k)
             ctx.has_seqused_k = seqused_k is not None
@@ -254,7 +275,17 @@ def flash_attn_func(q, k, v, softmax_scale=None, causal=False, qv=None, q_descal
                     v_descale=None, window_size=(-1, -1), attention_chunk=0, softcap=0.0, num_splits=1, pack_gqa=None,
                     deterministic=False, sm_margin=0, return_attn_probs=False, scheduler_metadata=None):
     """q: (batch_size, seqlen, nheads, headdim); k, v: (batch_size, seqlen, nheads_k, headdim).
+    qv (batch_size, seqlen, nheads, headdim_v) adds qv . v to the scores (the
+    default scale is then (headdim + headdim_v) ** -0.5). pack_gqa = False
+    gives each query head its own row tiles (the same results to rounding).
     Returns out, or (out, softmax_lse (batch, nheads, seqlen)) when return_attn_probs."""
+    if qv is not None:
+        if softmax_scale is None:
+            softmax_scale = (q.shape[-1] + qv.shape[-1]) ** (-0.5)
+        return _qv_by_concat(lambda q2, k2, v2: FlashAttnFunc.apply(
+            q2, k2, v2, softmax_scale, causal, None, q_descale, k_descale, v_descale, window_size, attention_chunk,
+            softcap, num_splits, pack_gqa, deterministic, sm_margin, return_attn_probs, scheduler_metadata),
+            q, k, v, qv, return_attn_probs)
     return FlashAttnFunc.apply(q, k, v, softmax_scale, causal, qv, q_descale, k_descale, v_descale, window_size,
                                attention_chunk, softcap, num_splits, pack_gqa, deterministic, sm_margin,
                                return_attn_probs, scheduler_metadata)
@@ -266,7 +297,16 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
                            pack_gqa=None, deterministic=False, sm_margin=0, return_attn_probs=False,
                            scheduler_metadata=None):
     """q: (total_q, nheads, headdim); k, v: (total_k, nheads_k, headdim).
-    softmax_lse is (nheads, total_q)."""
+    softmax_lse is (nheads, total_q). qv (total_q, nheads, headdim_v) and
+    pack_gqa as in flash_attn_func."""
+    if qv is not None:
+        if softmax_scale is None:
+            softmax_scale = (q.shape[-1] + qv.shape[-1]) ** (-0.5)
+        return _qv_by_concat(lambda q2, k2, v2: FlashAttnVarlenFunc.apply(
+            q2, k2, v2, cu_seqlens_q, cu_seqlens_k, seqused_q, seqused_k, max_seqlen_q, max_seqlen_k,
+            softmax_scale, causal, None, q_descale, k_descale, v_descale, window_size, attention_chunk, softcap,
+            num_splits, pack_gqa, deterministic, sm_margin, return_attn_probs, scheduler_metadata),
+            q, k, v, qv, return_attn_probs)
     return FlashAttnVarlenFunc.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_q, seqused_k, max_seqlen_q,
                                      max_seqlen_k, softmax_scale, causal, qv, q_descale, k_descale, v_descale,
                                      window_size, attention_chunk, softcap, num_splits, pack_gqa, deterministic,
@@ -313,9 +353,8 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None, rotary
     tensors)."""
     assert k_cache.stride(-1) == 1, "k_cache must have contiguous last dimension"
     assert v_cache.stride(-1) == 1, "v_cache must have contiguous last dimension"
-    _reject(qv=qv)
     if softmax_scale is None:
-        softmax_scale = q.shape[-1] ** (-0.5)
+        softmax_scale = (q.shape[-1] + (qv.shape[-1] if qv is not None else 0)) ** (-0.5)
     batch = q.shape[0] if cu_seqlens_q is None else cu_seqlens_q.numel() - 1
     if cache_seqlens is not None and isinstance(cache_seqlens, int):
         cache_seqlens = torch.full((batch,), cache_seqlens, dtype=torch.int32, device=k_cache.device)
@@ -338,14 +377,15 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None, rotary
         # cache indexed by the prefix sums of cache_seqlens
         # (csrc/arch22/flash_attn_npu_v3/flash_api.cpp:431-441 in the reference)
         _reject(k=k, v=v, rotary_cos=rotary_cos, cache_batch_idx=cache_batch_idx, cache_leftpad=cache_leftpad,
-                cu_seqlens_k_new=cu_seqlens_k_new)
+                cu_seqlens_k_new=cu_seqlens_k_new, qv=qv)
         if cache_seqlens is None:
             raise RuntimeError("cache_seqlens is required with cu_seqlens_q")
         cu_k = _cu_from_lengths(cache_seqlens)
         out, softmax_lse = ops.varlen_fwd(q, k_cache, v_cache, cu_seqlens_q, cu_k, cache_seqlens, None, None,
                                           int(max_seqlen_q), int(k_cache.shape[0]), 0.0, float(softmax_scale),
                                           bool(causal), int(window_size[0]), int(window_size[1]), float(softcap),
-                                          int(attention_chunk), q_descale, k_descale, v_descale, int(num_splits), ws)
+                                          int(attention_chunk), q_descale, k_descale, v_descale, int(num_splits), ws,
+                                          _pack(pack_gqa))
     else:
         # (batch, seqlen) or ragged (total_q) queries against a (batch_cache,
         # seqlen_cache) or paged cache, with the in-place append of k / v
@@ -358,7 +398,7 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None, rotary
                                               float(softmax_scale), bool(causal), int(window_size[0]),
                                               int(window_size[1]), int(attention_chunk), float(softcap),
                                               bool(rotary_interleaved), int(num_splits), q_descale, k_descale,
-                                              v_descale, ws)
+                                              v_descale, ws, maybe_contiguous(qv), _pack(pack_gqa))
     if return_softmax_lse:
         oa, la = _empty_accum(out)
         return out, softmax_lse, oa, la

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define FA_MI355X_ABI_VERSION 3
+#define FA_MI355X_ABI_VERSION 4
 
 typedef enum {
     FA_OK = 0,
@@ -175,6 +175,27 @@ typedef struct fa_fwd_params {
     int64_t k_descale_batch_stride, k_descale_head_stride;
     const float* v_descale;
     int64_t v_descale_batch_stride, v_descale_head_stride;
+
+    /* ---- qv and pack_gqa of the v3 API (ABI 4) ----
+       flash_attn_npu_v3/interface_arch22.py:940-962 declares both; the
+       reference kernels ignore qv (csrc/arch22/flash_attn_npu_v3/flash_api.cpp:66
+       takes q_v_ and never reads it) and reject pack_gqa = True (:162). The
+       semantics here are FlashAttention-3's:
+         scores = softmax_scale * (q . k + qv . v)
+       qv is (B, Sq, H, Dv), or (total_q, H, Dv) with cu_seqlens_q, in the
+       dtype of q (16-bit only). It is taken by the decode kernel: at most 16
+       query rows per kv head (seqlen_q * H / Hk, or seqlen_q with
+       no_pack_gqa) and headdim <= 128; other shapes return FA_EUNSUPPORTED. */
+    const void* qv;
+    int64_t qv_batch_stride, qv_row_stride, qv_head_stride;
+    /* nonzero (pack_gqa = False): each query head gets its own row tiles
+       instead of sharing them with the other query heads of its kv head
+       (GQA packing, the default). The results agree to rounding, not bit
+       for bit: a wave rescales its rows' running maxima together when any
+       of them needs it, so a row's rounding depends on the rows that share
+       its wave, and the split-KV cuts may differ. The kv heads are then
+       read once per query head instead of once. */
+    int32_t no_pack_gqa;
 } fa_fwd_params;
 
 /* Library / ABI version. */

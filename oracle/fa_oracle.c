@@ -175,6 +175,17 @@ static void attention_row(const orc_fwd_params* p, int b, int i, int h, int sq, 
     const uint16_t* q = p->q + qrow + (int64_t)h * p->q_sh;
     float qf[1024];
     for (int d = 0; d < D; d++) qf[d] = to_f32(dt, q[d]);
+    /* qv (FlashAttention-3, flash_attn_npu_v3/interface_arch22.py:1018 of the
+     * reference): the score of key j adds qv . v_j, summed after q . k_j in
+     * the same fp32 accumulator, i.e. the score of the concatenations [q, qv]
+     * and [k_j, v_j] */
+    float qvf[1024];
+    if (p->qv) {
+        int64_t vrow = p->cu_seqlens_q ? ((int64_t)p->cu_seqlens_q[b] + i) * p->qv_si
+                                       : (int64_t)b * p->qv_sb + (int64_t)i * p->qv_si;
+        const uint16_t* qvr = p->qv + vrow + (int64_t)h * p->qv_sh;
+        for (int d = 0; d < Dv; d++) qvf[d] = to_f32(dt, qvr[d]);
+    }
     float slope = 0.f;
     if (p->alibi) slope = p->alibi[(int64_t)b * p->alibi_sb + h];
 
@@ -192,6 +203,10 @@ static void attention_row(const orc_fwd_params* p, int b, int i, int h, int sq, 
             const uint16_t* kr = key_row(p, b, j, hk, 0);
             float acc = 0.f;
             for (int d = 0; d < D; d++) acc += qf[d] * to_f32(dt, kr[d]);
+            if (p->qv) {
+                const uint16_t* vr = key_row(p, b, j, hk, 1);
+                for (int d = 0; d < Dv; d++) acc += qvf[d] * to_f32(dt, vr[d]);
+            }
             float x = acc * p->scale;
             if (p->softcap > 0.f) x = p->softcap * tanhf(x / p->softcap);
             if (p->alibi) {

@@ -29,6 +29,8 @@ typedef struct {
     float* lse; int64_t lse_sb, lse_sh;    /* (B,H,Sq) or, when varlen, (H,T) */
     int nthreads;
     int chunk;                             /* attention_chunk, 0 = off */
+    const uint16_t* qv; int64_t qv_sb, qv_si, qv_sh;  /* NULL, or the v3 qv (rows like q, Dv columns):
+                                                        the score adds qv . v */
 } orc_fwd_params;
 
 typedef struct {

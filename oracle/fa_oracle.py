@@ -47,6 +47,7 @@ class _FwdParams(ctypes.Structure):
         ("lse", _f32p), ("lse_sb", _i64), ("lse_sh", _i64),
         ("nthreads", ctypes.c_int),
         ("chunk", ctypes.c_int),
+        ("qv", _u16p), ("qv_sb", _i64), ("qv_si", _i64), ("qv_sh", _i64),
     ]
 
 
@@ -153,10 +154,11 @@ def normalize_window(seqlen_q, seqlen_k, causal, wl, wr):
 
 def attention(q, k, v, *, dtype, scale, softcap=0.0, causal=False, window=(-1, -1), alibi=None,
               seqlens_k=None, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q=None,
-              block_table=None, batch_idx=None, nthreads=1, chunk=0):
+              block_table=None, batch_idx=None, nthreads=1, chunk=0, qv=None):
     """Blockwise golden forward.
 
     q: (B, Sq, H, D) or, with cu_seqlens_q, (T, H, D) uint16 bits.
+    qv: None, or rows like q with v's head dim; the scores add qv . v.
     k, v: (Bc, Sk, Hk, D) contiguous caches, (num_blocks, page, Hk, D) with block_table,
           or (Tk, Hk, D) with cu_seqlens_k.
     Returns (out uint16 like q, lse float32 (B, H, Sq) or (H, T)).
@@ -231,6 +233,12 @@ def attention(q, k, v, *, dtype, scale, softcap=0.0, causal=False, window=(-1, -
         lse=_p(lse, ctypes.c_float), lse_sb=lse_sb, lse_sh=lse_sh,
         nthreads=nthreads, chunk=int(chunk),
     )
+    if qv is not None:
+        qv = np.ascontiguousarray(qv)
+        assert qv.shape[:-1] == q.shape[:-1] and qv.shape[-1] == Dv, "qv must be q's rows with v's head dim"
+        qst = ([0] + _st(qv)) if varlen_q else _st(qv)
+        p.qv = _p(qv, ctypes.c_uint16)
+        p.qv_sb, p.qv_si, p.qv_sh = qst[0], qst[1], qst[2]
     rc = lib().orc_attention(ctypes.byref(p))
     if rc != 0:
         raise ValueError("oracle rejected the shapes")
@@ -388,7 +396,7 @@ def kvcache_forward_v3(q, k_cache, v_cache, *, dtype, cache_seqlens, k=None, v=N
                        rotary_sin=None, rotary_interleaved=True, cache_batch_idx=None, block_table=None,
                        softmax_scale=None, causal=False, window=(-1, -1), softcap=0.0, alibi=None,
                        cache_leftpad=None, rotary_seqlens=None, cu_seqlens_q=None, max_seqlen_q=None,
-                       cu_seqlens_k_new=None, attention_chunk=0, nthreads=1):
+                       cu_seqlens_k_new=None, attention_chunk=0, nthreads=1, qv=None):
     """The v3 flash_attn_with_kvcache contract (README.md:311-401 of the
     reference, whose kernels reject the extensions), one sequence at a time:
 
@@ -402,7 +410,9 @@ def kvcache_forward_v3(q, k_cache, v_cache, *, dtype, cache_seqlens, k=None, v=N
         lp = cache_leftpad (default 0): attention runs on the cache with its
         first lp_b slots removed, so masks count keys from lp_b;
       * attention_chunk c > 0 also restricts query i to the chunk of its
-        diagonal key.
+        diagonal key;
+      * qv (rows like q, v's head dim) adds qv . v to the scores, and the
+        default scale is then (D + Dv) ** -0.5 (FlashAttention-3).
 
     Built from the pinned primitives kv_append, rotary and attention.
     Returns (out, lse, k_cache_after, v_cache_after); lse is (B, H, Sq), or
@@ -412,7 +422,7 @@ def kvcache_forward_v3(q, k_cache, v_cache, *, dtype, cache_seqlens, k=None, v=N
     B = len(cu_q) - 1 if ragged_q else q.shape[0]
     H, D = q.shape[-2], q.shape[-1]
     if softmax_scale is None:
-        softmax_scale = D ** -0.5
+        softmax_scale = (D + (qv.shape[-1] if qv is not None else 0)) ** -0.5
     L = np.asarray(cache_seqlens, dtype=np.int64)
     P = L if rotary_seqlens is None else np.asarray(rotary_seqlens, dtype=np.int64)
     lp = np.zeros(B, np.int64) if cache_leftpad is None else np.asarray(cache_leftpad, dtype=np.int64)
@@ -439,6 +449,7 @@ def kvcache_forward_v3(q, k_cache, v_cache, *, dtype, cache_seqlens, k=None, v=N
                                    block_table=block_table, cos=rotary_cos, sin=rotary_sin,
                                    interleaved=rotary_interleaved, rot_pos=P[b:b + 1])
         qb = q[cu_q[b]:cu_q[b + 1]][None] if ragged_q else q[b:b + 1]
+        qvb = None if qv is None else (qv[cu_q[b]:cu_q[b + 1]][None] if ragged_q else qv[b:b + 1])
         if qb.shape[1] == 0:
             continue
         if k is not None and rotary_cos is not None:
@@ -455,7 +466,8 @@ def kvcache_forward_v3(q, k_cache, v_cache, *, dtype, cache_seqlens, k=None, v=N
             ab = al[b] if al.ndim == 2 else al
         ob, lb = attention(qb, kv_k, kv_v, dtype=dtype, scale=softmax_scale, softcap=softcap, causal=causal,
                            window=window, alibi=ab, seqlens_k=np.array([L[b] + s_new - lp[b]]),
-                           block_table=block_table, batch_idx=bidx, nthreads=nthreads, chunk=attention_chunk)
+                           block_table=block_table, batch_idx=bidx, nthreads=nthreads, chunk=attention_chunk,
+                           qv=qvb)
         if ragged_q:
             out[cu_q[b]:cu_q[b + 1]] = ob[0]
             lse[:, cu_q[b]:cu_q[b + 1]] = lb[0]

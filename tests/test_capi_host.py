@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(capi):
     for n in names:
         assert hasattr(lib, n), f"libfa_mi355x.so does not export {n}"
     assert sorted(capi.EXPORTED) == names
-    assert capi.lib().fa_abi_version() == capi.ABI_VERSION == 3
+    assert capi.lib().fa_abi_version() == capi.ABI_VERSION == 4
 
 
 @pytest.mark.parametrize("struct", ["fa_fwd_params", "fa_bwd_params"])
@@ -131,6 +131,17 @@ def test_validate_accepts_a_valid_call(capi):
                                     k_descale=0x12000, v_descale=0x13000), capi.FA_KIND_DENSE) == capi.FA_OK, d
 
 
+QV = dict(qv=0x15000, qv_batch_stride=1024, qv_row_stride=1024, qv_head_stride=128)
+
+
+def test_validate_qv_where_the_decode_kernel_runs(capi):
+    # rows per kv head = seqlen_q * nheads / nheads_k with packed GQA, seqlen_q without
+    assert capi.validate(_valid(capi, seqlen_q=4, **QV), capi.FA_KIND_KVCACHE) == capi.FA_OK, capi.last_error()
+    assert capi.validate(_valid(capi, seqlen_q=2, **QV), capi.FA_KIND_DENSE) == capi.FA_OK, capi.last_error()
+    assert capi.validate(_valid(capi, seqlen_q=16, no_pack_gqa=1, **QV), capi.FA_KIND_KVCACHE) == capi.FA_OK
+    assert capi.validate(_valid(capi, seqlen_q=16, **QV), capi.FA_KIND_KVCACHE) == capi.FA_EUNSUPPORTED
+
+
 BAD = [
     # (field overrides, kind, expected status, message fragment)
     (dict(abi_version=7), 0, "EINVAL", "abi_version"),
@@ -165,6 +176,11 @@ BAD = [
           rotary_cos=0x90000, rotary_sin=0xA0000, rotary_dim=64, seqlen_ro=16), 0, "EINVAL",
      "rotary is not supported with FP8"),
     (dict(dtype=4), 1, "EINVAL", "only support fp16 and bf16"),
+    (dict(dtype=3, **QV), 0, "EINVAL", "qv is not supported with FP8"),
+    (dict(QV, qv=0x15008), 0, "EINVAL", "qv must be 16-byte aligned"),
+    (dict(QV, qv_row_stride=1020), 0, "EINVAL", "qv must be 16-byte aligned"),
+    (dict(seqlen_q=5, **QV), 0, "EUNSUPPORTED", "qv is supported where the decode kernel runs"),
+    (dict(headdim=192, headdim_v=192, **QV), 1, "EUNSUPPORTED", "qv is supported where the decode kernel runs"),
 ]
 
 

@@ -544,3 +544,52 @@ def test_bf16_conversions_vs_torch():
     ref = torch.from_numpy(xs).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(got, ref)
     assert np.array_equal(orc.to_bits(xs, orc.BF16), ref)
+
+
+# ---- qv (FlashAttention-3: scores = q.k + qv.v) --------------------------------------------
+@pytest.mark.parametrize("dt", [orc.FP16, orc.BF16])
+def test_qv_is_attention_over_concatenated_head_dims(dt):
+    # the oracle accumulates q.k then qv.v in one fp32 sum: the same bits as
+    # [q, qv] . [k, v] over the concatenated head dims
+    rng = np.random.default_rng(71)
+    B, Sq, Sk, H, Hk, D = 2, 3, 600, 8, 2, 64
+    q, qv = rbits(rng, (B, Sq, H, D), dt), rbits(rng, (B, Sq, H, D), dt)
+    k, v = rbits(rng, (B, Sk, Hk, D), dt), rbits(rng, (B, Sk, Hk, D), dt)
+    scale = (2 * D) ** -0.5
+    o1, l1 = orc.attention(q, k, v, dtype=dt, scale=scale, causal=True, qv=qv, nthreads=NT)
+    o2, l2 = orc.attention(np.concatenate([q, qv], -1), np.concatenate([k, v], -1), v, dtype=dt, scale=scale,
+                           causal=True, nthreads=NT)
+    assert np.array_equal(o1, o2) and np.array_equal(l1, l2)
+
+
+def test_qv_vs_fp64_brute_force():
+    rng = np.random.default_rng(72)
+    dt = orc.BF16
+    B, Sq, Sk, H, Hk, D = 2, 4, 530, 8, 2, 128
+    q, qv = rbits(rng, (B, Sq, H, D), dt), rbits(rng, (B, Sq, H, D), dt)
+    k, v = rbits(rng, (B, Sk, Hk, D), dt), rbits(rng, (B, Sk, Hk, D), dt)
+    scale = (2 * D) ** -0.5
+    out, lse = orc.attention(q, k, v, dtype=dt, scale=scale, causal=True, window=(200, 0), qv=qv, nthreads=NT)
+    qf, qvf, kf, vf = f(q, dt), f(qv, dt), f(k, dt), f(v, dt)
+    ro, rl = brute.attention_batch(np.concatenate([qf, qvf], -1), np.concatenate([kf, vf], -1), vf, [Sk] * B,
+                                   scale, True, (200, 0))
+    check_vs_brute(out, lse, ro, rl, dt)
+    # and the qv term matters: without it the output moves well past the tolerance
+    o0, _ = orc.attention(q, k, v, dtype=dt, scale=scale, causal=True, window=(200, 0), nthreads=NT)
+    assert np.abs(f(o0, dt) - ro).max() > 10 * TOL[dt]
+
+
+def test_qv_varlen_rows_follow_cu_seqlens_q():
+    rng = np.random.default_rng(73)
+    dt = orc.FP16
+    D, H, Hk = 64, 4, 2
+    cu = np.array([0, 3, 3, 7], dtype=np.int32)
+    q, qv = rbits(rng, (7, H, D), dt), rbits(rng, (7, H, D), dt)
+    k, v = rbits(rng, (3, 90, Hk, D), dt), rbits(rng, (3, 90, Hk, D), dt)
+    seqlens = np.array([90, 50, 20], dtype=np.int32)
+    o, l = orc.attention(q, k, v, dtype=dt, scale=0.1, causal=True, cu_seqlens_q=cu, seqlens_k=seqlens, qv=qv)
+    for b in (0, 2):
+        ob, lb = orc.attention(q[None, cu[b]:cu[b + 1]], k[b:b + 1, :seqlens[b]], v[b:b + 1, :seqlens[b]],
+                               dtype=dt, scale=0.1, causal=True, qv=qv[None, cu[b]:cu[b + 1]])
+        assert np.array_equal(o[cu[b]:cu[b + 1]], ob[0])
+        assert np.array_equal(l[:, cu[b]:cu[b + 1]], lb[0])
