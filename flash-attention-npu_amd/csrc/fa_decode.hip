@@ -63,6 +63,7 @@ struct DecCfg {
 struct DecSeg {
     int S, n;         // first global tile, tiles
     int b, hk;
+    int kvh;          // kv head of the segment's row tile (hk, or hk / kvdiv unpacked)
     int lo_tile;      // first 32-key tile of the sequence's visible key range
     int sk, sq, crow;
     int lp;           // cache_leftpad: key j is cache row lp + j (contiguous caches)
@@ -111,6 +112,7 @@ __device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref
     const int o = t - s_pref[bl];
     s.hk = per > 0 ? o / per : 0;
     s.S = s_pref[bl] + s.hk * per;
+    s.kvh = a.kvdiv == 1 ? s.hk : s.hk / a.kvdiv;
     const DecBatch d = s_b[bl];
     s.lo_tile = d.lo_tile;
     s.sk = d.sk;
@@ -124,16 +126,19 @@ __device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref
 // BIAS: softcap or ALiBi present; FUSE: append k_new/v_new in this kernel;
 // LAYOUT: 0 = batch-strided cache, 1 = paged with page % 32 == 0, 2 = any;
 // HDM: head dim below 128 (dims >= a.hd read as zero, never written).
+// QV: the scores add qv . v (one more MFMA chain per 16 keys, V against the
+// qv row, into the same accumulator); 16-bit inputs only.
 // DT_FP8: the cache, q and k_new / v_new hold e4m3fn bytes. The register
 // pipeline carries the raw bytes (half the registers and half the HBM bytes
 // of a bf16 cache). S^T = K.Q^T runs as 16x16x128 e4m3 MFMAs on those bytes;
 // V is widened to bf16 on its way into the wave's LDS tile, and P.V stays a
 // bf16 product. The descales scale the scores (q_descale * k_descale) and
 // the output (v_descale).
-template <int DT, int HD, int STAGES, bool BIAS, bool FUSE, int LAYOUT, bool HDM = false>
+template <int DT, int HD, int STAGES, bool BIAS, bool FUSE, int LAYOUT, bool HDM = false, bool QV = false>
 __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     using namespace dec;
     constexpr bool F8 = DT == DT_FP8;
+    static_assert(!(QV && F8), "qv takes 16-bit inputs");
     using C = DecCfg<HD, F8 ? 1 : 2>;
     constexpr int D = C::D, KT = C::KT, NH = C::NH, KSTEPS = C::KSTEPS, DBLK = C::DBLK;
     using ET = std::conditional_t<F8, uint8_t, uint16_t>;  // stored element
@@ -236,11 +241,11 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                 b2 = min(max(a.block_table[(int64_t)s.crow * a.bt_stride + pidx], 0), a.num_blocks - 1);
             }
             const int inpage = a.page_shift >= 0 ? (key & (a.page - 1)) : key % a.page;
-            return base + (int64_t)b2 * sb + (int64_t)inpage * si + (int64_t)(s.hk / a.kvdiv) * sh;
+            return base + (int64_t)b2 * sb + (int64_t)inpage * si + (int64_t)s.kvh * sh;
         }
         if (LAYOUT == 2 && a.cu_seqlens_k)
-            return base + ((int64_t)a.cu_seqlens_k[s.b] + key) * si + (int64_t)(s.hk / a.kvdiv) * sh;
-        return base + (int64_t)s.crow * sb + (int64_t)(s.lp + key) * si + (int64_t)(s.hk / a.kvdiv) * sh;
+            return base + ((int64_t)a.cu_seqlens_k[s.b] + key) * si + (int64_t)s.kvh * sh;
+        return base + (int64_t)s.crow * sb + (int64_t)(s.lp + key) * si + (int64_t)s.kvh * sh;
     };
 
     // With a fused append, keys nf .. sk - 1 come from k_new / v_new; the
@@ -273,7 +278,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                 const ET* vpr;
                 if (key >= first_new) {
                     const int tn = key - first_new;
-                    const int64_t kvh = is.hk / a.kvdiv;
+                    const int64_t kvh = is.kvh;
                     kpr = knp + (int64_t)is.b * a.kn_sb + (int64_t)tn * a.kn_si + kvh * a.kn_sh + G * (D / 4);
                     vpr = vnp + (int64_t)is.b * a.vn_sb + (int64_t)tn * a.vn_si + kvh * a.vn_sh + G * (D / 4);
                 } else {
@@ -299,7 +304,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     // ---- compute side --------------------------------------------------------------------
     DecSeg cs = dec_seg_of(a, s_pref, s_bat, t0);
     u32x4 qreg[KSTEPS];
-    u32x4 qvreg[KSTEPS];  // qv rows (16-bit inputs with qv only)
+    u32x4 qvreg[QV ? KSTEPS : 1];  // QV: the qv row
     u32x4 q8[2];  // FP8: the raw q bytes of dims G * D / 4 .. + D / 4 (zero-padded to 32)
     float slope = 0.f;
     int qi = 0;
@@ -334,7 +339,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                 const bool in = ok && (!HDM || (G * KSTEPS + s2) * 8 < a.hd);
                 qreg[s2] = in ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s2) * 8) : u32x4{0u, 0u, 0u, 0u};
             }
-            if (a.qv) {
+            if constexpr (QV) {
                 // qv row of the same (position, head): B operand against V, as q against K
                 const ET* qvp = static_cast<const ET*>(a.qv);
                 const ET* qvrow = a.cu_seqlens_q
@@ -348,7 +353,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             }
         }
         if constexpr (F8) {
-            const int kvh = s.hk / a.kvdiv;
+            const int kvh = s.kvh;
             const float qk = descale_at(a.qd, a.qd_sb, a.qd_sh, s.b, kvh) * descale_at(a.kd, a.kd_sb, a.kd_sh, s.b, kvh);
             sc_qk = a.scale * qk;
             sc_qk2 = a.scale_log2 * qk;
@@ -453,7 +458,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
                 for (int h = 0; h < NH; ++h) sacc[h] = mfma16x16x32<DT>(opnd(kk, h, s), qreg[s], sacc[h]);
-            if (a.qv) {
+            if constexpr (QV) {
                 // S^T += V . Qv^T: the V loads carry the same lane layout as the K loads
 #pragma unroll
                 for (int s = 0; s < KSTEPS; ++s)
@@ -713,10 +718,18 @@ static void launch_decode_l(const FwdArgs& a, int grid, hipStream_t stream) {
 template <int DT, int HD>
 static void launch_decode_t(const FwdArgs& a, int grid, hipStream_t stream) {
     constexpr int KT = DecCfg<HD, DT == DT_FP8 ? 1 : 2>::KT;
+    constexpr int S = DT == DT_FP8 ? kDecodeStagesF8 : kDecodeStages;
+    if constexpr (DT != DT_FP8) {
+        if (a.qv) {
+            // qv: the generic-layout, bias-capable, dim-masking instances
+            if (a.k_new) hipLaunchKernelGGL((fa_decode_kernel<DT, HD, S, true, true, 2, true, true>), dim3(grid), dim3(256), 0, stream, a);
+            else hipLaunchKernelGGL((fa_decode_kernel<DT, HD, S, true, false, 2, true, true>), dim3(grid), dim3(256), 0, stream, a);
+            return;
+        }
+    }
     if (a.hd < HD) {
         // head dims below the kernel's: the generic-layout, bias-capable
         // instances with dim masking (correct for every input of this kernel)
-        constexpr int S = DT == DT_FP8 ? kDecodeStagesF8 : kDecodeStages;
         if (a.k_new) hipLaunchKernelGGL((fa_decode_kernel<DT, HD, S, true, true, 2, true>), dim3(grid), dim3(256), 0, stream, a);
         else hipLaunchKernelGGL((fa_decode_kernel<DT, HD, S, true, false, 2, true>), dim3(grid), dim3(256), 0, stream, a);
         return;
