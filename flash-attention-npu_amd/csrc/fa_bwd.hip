@@ -53,12 +53,14 @@ struct BwCfg {
     static constexpr int BK = KNW * 16 * KRB;
     static constexpr int BQ = 64;
     static constexpr int CPQ = BQ * DCH / KNT;  // chunks per thread per q (and dout) tile
-    // dQ kernel: 1 row block of 16 per wave (q, dout and dQ^T of two would
-    // not fit 256 VGPRs at two waves per SIMD); 8 waves and 64-key tiles at
-    // 128, one wave per SIMD and 32-key tiles at 256
+    // dQ kernel: 2 row blocks of 16 per wave up to head dim 128, so every
+    // K / V operand read from LDS feeds twice the products (the kernel is
+    // bound by LDS reads; at 128 a few values spill, still 3053 -> 2762 us
+    // for the whole backward of B4 S4096 H32/8 causal); 8 waves and 64-key
+    // tiles up to 128, one wave per SIMD, 1 row block and 32-key tiles at 256
     static constexpr int QNW = HD > 128 ? 4 : 8;
     static constexpr int QNT = QNW * 64;
-    static constexpr int RB = HD == 64 ? 2 : 1;
+    static constexpr int RB = HD <= 128 ? 2 : 1;
     static constexpr int BM = QNW * RB * 16;
     static constexpr int BN = HD > 128 ? 32 : 64;
     static constexpr int CPK = BN * DCH / QNT;
