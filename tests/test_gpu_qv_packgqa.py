@@ -27,10 +27,10 @@ NT = min(16, os.cpu_count() or 1)
 
 
 def _kvcache_case(*, B, Sq, H, Hk, D, dtype, L, capacity=0, page=0, new=0, window=(-1, -1), ragged=None,
-                  pack_gqa=None, seed=0, with_qv=True):
+                  pack_gqa=None, seed=0, with_qv=True, softcap=0.0):
     import flash_attn_npu_v3
     print(f"case qv kvcache B{B} Sq{Sq} H{H}/{Hk} D{D} page{page} new{new} win{window} ragged{ragged} "
-          f"pack{pack_gqa} qv{with_qv}", flush=True)
+          f"pack{pack_gqa} qv{with_qv} softcap{softcap}", flush=True)
     g = torch.Generator().manual_seed(seed)
     if ragged is not None:
         cu_q = np.concatenate([[0], np.cumsum(ragged)]).astype(np.int32)
@@ -60,7 +60,7 @@ def _kvcache_case(*, B, Sq, H, Hk, D, dtype, L, capacity=0, page=0, new=0, windo
     ro, rl, rk, _ = orc.kvcache_forward_v3(
         bits(q), bits(kc), bits(vc), dtype=odt(dtype), cache_seqlens=L,
         k=None if kn is None else bits(kn), v=None if vn is None else bits(vn),
-        block_table=None if bt is None else bt.numpy(), causal=True, window=window,
+        block_table=None if bt is None else bt.numpy(), causal=True, window=window, softcap=softcap,
         cu_seqlens_q=cu_q, max_seqlen_q=None if ragged is None else int(max(ragged)),
         qv=None if qv is None else bits(qv), nthreads=NT)
     kc_d, vc_d = kc.to(DEV), vc.to(DEV)
@@ -70,7 +70,7 @@ def _kvcache_case(*, B, Sq, H, Hk, D, dtype, L, capacity=0, page=0, new=0, windo
         cache_seqlens=torch.from_numpy(L).to(DEV), page_table=None if bt is None else bt.to(DEV),
         cu_seqlens_q=None if cu_q is None else torch.from_numpy(cu_q).to(DEV),
         max_seqlen_q=None if ragged is None else int(max(ragged)), causal=True, window_size=window,
-        pack_gqa=pack_gqa, return_softmax_lse=True)
+        softcap=softcap, pack_gqa=pack_gqa, return_softmax_lse=True)
     torch.cuda.synchronize()
     assert_close_out(out, ro, dtype)
     assert_close_lse(lse, rl)
@@ -84,12 +84,38 @@ QV_KV = [
     dict(B=3, Sq=2, H=8, Hk=2, D=128, dtype=torch.bfloat16, L=[100, 500, 64], capacity=512, ragged=[2, 1, 2]),
     dict(B=2, Sq=1, H=8, Hk=1, D=96, dtype=torch.bfloat16, L=[1000, 77], capacity=1024, new=1),
     dict(B=2, Sq=4, H=32, Hk=8, D=128, dtype=torch.bfloat16, L=[400, 1500], page=256, pack_gqa=False),
+    # soft capping: qv . v enters the capped score
+    dict(B=3, Sq=1, H=16, Hk=4, D=128, dtype=torch.bfloat16, L=[900, 40, 1700], capacity=2048, new=1, softcap=5.0),
+    dict(B=2, Sq=2, H=8, Hk=2, D=64, dtype=torch.float16, L=[333, 1200], page=64, window=(100, 0), softcap=2.0),
 ]
 
 
 @pytest.mark.parametrize("case", QV_KV, ids=[str(i) for i in range(len(QV_KV))])
 def test_qv_kvcache_decode_vs_oracle(case):
     _kvcache_case(seed=500, **case)
+
+
+def test_qv_decode_with_alibi_through_the_op():
+    # the v3 Python API has no alibi_slopes; the operator does (the decode
+    # kernel's qv instance forms its scores explicitly, ALiBi included)
+    from fa_mi355x import ops
+    print("case qv decode + ALiBi (op)", flush=True)
+    g = torch.Generator().manual_seed(560)
+    B, H, Hk, D, dtype = 3, 16, 4, 128, torch.bfloat16
+    L = np.array([1200, 77, 600], np.int32)
+    q, qv = randn((B, 2, H, D), dtype, g, "cpu"), randn((B, 2, H, D), dtype, g, "cpu")
+    kc, vc = randn((B, 1536, Hk, D), dtype, g, "cpu"), randn((B, 1536, Hk, D), dtype, g, "cpu")
+    slopes = (2.0 ** (-8.0 * (torch.arange(H) + 1) / H)).float()
+    scale = (2 * D) ** -0.5
+    ro, rl, _, _ = orc.kvcache_forward_v3(bits(q), bits(kc), bits(vc), dtype=orc.BF16, cache_seqlens=L,
+                                          softmax_scale=scale, causal=True, alibi=slopes.numpy(), qv=bits(qv),
+                                          nthreads=NT)
+    out, lse = ops.fwd_kvcache_v3(q.to(DEV), kc.to(DEV), vc.to(DEV), None, None, torch.from_numpy(L).to(DEV), None,
+                                  None, None, None, None, slopes.to(DEV), None, None, 0, None, scale, True, -1, 0, 0,
+                                  0.0, True, 0, None, None, None, None, qv.to(DEV), None)
+    torch.cuda.synchronize()
+    assert_close_out(out, ro, dtype)
+    assert_close_lse(lse, rl)
 
 
 def test_qv_rejected_where_the_decode_kernel_does_not_run():

@@ -547,18 +547,22 @@ def test_bf16_conversions_vs_torch():
 
 
 # ---- qv (FlashAttention-3: scores = q.k + qv.v) --------------------------------------------
-@pytest.mark.parametrize("dt", [orc.FP16, orc.BF16])
-def test_qv_is_attention_over_concatenated_head_dims(dt):
-    # the oracle accumulates q.k then qv.v in one fp32 sum: the same bits as
-    # [q, qv] . [k, v] over the concatenated head dims
+@pytest.mark.parametrize("dt,softcap,alibi", [(orc.FP16, 0.0, False), (orc.BF16, 0.0, False),
+                                               (orc.BF16, 4.0, False), (orc.FP16, 0.0, True)])
+def test_qv_is_attention_over_concatenated_head_dims(dt, softcap, alibi):
+    # the oracle accumulates q.k then qv.v in one fp32 sum, before the scale,
+    # the soft cap and the ALiBi bias: the same bits as [q, qv] . [k, v] over
+    # the concatenated head dims
     rng = np.random.default_rng(71)
     B, Sq, Sk, H, Hk, D = 2, 3, 600, 8, 2, 64
     q, qv = rbits(rng, (B, Sq, H, D), dt), rbits(rng, (B, Sq, H, D), dt)
     k, v = rbits(rng, (B, Sk, Hk, D), dt), rbits(rng, (B, Sk, Hk, D), dt)
     scale = (2 * D) ** -0.5
-    o1, l1 = orc.attention(q, k, v, dtype=dt, scale=scale, causal=True, qv=qv, nthreads=NT)
+    sl = (2.0 ** (-8.0 * (np.arange(H) + 1) / H)).astype(np.float32) if alibi else None
+    o1, l1 = orc.attention(q, k, v, dtype=dt, scale=scale, causal=True, qv=qv, softcap=softcap, alibi=sl,
+                           nthreads=NT)
     o2, l2 = orc.attention(np.concatenate([q, qv], -1), np.concatenate([k, v], -1), v, dtype=dt, scale=scale,
-                           causal=True, nthreads=NT)
+                           causal=True, softcap=softcap, alibi=sl, nthreads=NT)
     assert np.array_equal(o1, o2) and np.array_equal(l1, l2)
 
 
@@ -577,6 +581,11 @@ def test_qv_vs_fp64_brute_force():
     # and the qv term matters: without it the output moves well past the tolerance
     o0, _ = orc.attention(q, k, v, dtype=dt, scale=scale, causal=True, window=(200, 0), nthreads=NT)
     assert np.abs(f(o0, dt) - ro).max() > 10 * TOL[dt]
+    # soft capping applies to the whole score q.k + qv.v
+    out, lse = orc.attention(q, k, v, dtype=dt, scale=scale, causal=True, qv=qv, softcap=3.0, nthreads=NT)
+    ro, rl = brute.attention_batch(np.concatenate([qf, qvf], -1), np.concatenate([kf, vf], -1), vf, [Sk] * B,
+                                   scale, True, softcap=3.0)
+    check_vs_brute(out, lse, ro, rl, dt)
 
 
 def test_qv_varlen_rows_follow_cu_seqlens_q():
