@@ -81,11 +81,11 @@ def test_v3_shim_positional():
     none8 = (None,) * 8
 
     def call(q, k, v, k_new=None, v_new=None, cu_q=None, cu_k=None, seqused_k=None, max_q=None, max_k=None,
-             page_table=None, causal=True, md=None, num_splits=1):
+             page_table=None, causal=True, md=None, num_splits=1, qv=None, pack_gqa=None):
         # the positional order of flash_attn_npu_v3/interface_arch22.py:111-146
-        return m.fwd(q, k, v, k_new, v_new, None, None, cu_q, cu_k, None, None, seqused_k, max_q, max_k, page_table,
+        return m.fwd(q, k, v, k_new, v_new, qv, None, cu_q, cu_k, None, None, seqused_k, max_q, max_k, page_table,
                      None, None, None, None, None, None, None, None, s, causal, -1, -1, 0, 0.0, True, md, num_splits,
-                     None, 0)
+                     pack_gqa, 0)
 
     o, l, oa, la = call(q, k, v)
     ro, rl = api.flash_attn_func(q, k, v, causal=True, return_attn_probs=True)
@@ -106,6 +106,15 @@ def test_v3_shim_positional():
     ro, rl, *_ = api.flash_attn_with_kvcache(qk, kc2, vc2, k=kn, v=vn, cache_seqlens=sl, causal=True,
                                              return_softmax_lse=True)
     assert _eq(o, ro) and _eq(l, rl) and _eq(kc, kc2) and _eq(vc, vc2)
+    # qv (the reference's q_v_ argument) on a decode call, and pack_gqa = False
+    qd1, qvd = randn((3, 1, 32, 128), dt, g, DEV), randn((3, 1, 32, 128), dt, g, DEV)
+    o, l, _, _ = call(qd1, kc, vc, seqused_k=sl, qv=qvd, num_splits=0)
+    ro, rl, *_ = api.flash_attn_with_kvcache(qd1, kc, vc, qv=qvd, cache_seqlens=sl, softmax_scale=s, causal=True,
+                                             return_softmax_lse=True)
+    assert _eq(o, ro) and _eq(l, rl)
+    o, l, _, _ = call(q, k, v, pack_gqa=False)
+    ro, rl = api.flash_attn_func(q, k, v, causal=True, pack_gqa=False, return_attn_probs=True)
+    assert _eq(o, ro) and _eq(l, rl)
     # bwd(dout, q, k, v, out, lse, dq_, dk_, dv_, cu_q, cu_k, seqused_q, seqused_k, max_q, max_k, scale, causal,
     #     wl, wr, softcap, deterministic, sm_margin)
     o, l, _, _ = call(q, k, v)
