@@ -29,6 +29,7 @@ namespace dec {
 constexpr int NWAVE = 4;     // waves (workers) per workgroup
 constexpr int TABN = 256;    // paged: block ids staged per wave
 constexpr int MAXB = 2048;
+constexpr int MERGE_SPLIT = 4;  // merge workgroups per segment, each merging D / MERGE_SPLIT dims
 }  // namespace dec
 
 #ifdef FA_DECODE_PHASES
@@ -594,7 +595,7 @@ __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int wor
     using namespace dec;
     __shared__ __attribute__((aligned(16))) float s_acc[256][8];
     __shared__ float s_gm[256], s_gs[256];
-    constexpr int DSPLIT = 4;            // workgroups per segment, each merging D / DSPLIT dims
+    constexpr int DSPLIT = MERGE_SPLIT;
     constexpr int CH = D / DSPLIT / 8;   // 8-dim chunks per row in one workgroup
     const int sig = blockIdx.x / DSPLIT, dsl = blockIdx.x % DSPLIT;
     const int b = sig / a.Hk, hk = sig % a.Hk;
@@ -757,7 +758,7 @@ hipError_t launch_decode(const FwdArgs& a, int dtype, int d, int grid, hipStream
 
 hipError_t launch_decode_merge(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream) {
     if (d != 64 && d != 128) return hipErrorInvalidValue;
-    const int segs = a.B * a.Hk * 4;  // DSPLIT workgroups per (sequence, kv head) segment
+    const int segs = a.B * a.Hk * dec::MERGE_SPLIT;  // workgroups: MERGE_SPLIT per (sequence, kv head) segment
     const int w = grid * dec::NWAVE;
     if (dtype == DT_BF16 || dtype == DT_FP8) {  // FP8 inputs give a bf16 output
         if (d == 64) hipLaunchKernelGGL((fa_decode_merge_kernel<DT_BF16, 64>), dim3(segs), dim3(256), 0, stream, a, w);
