@@ -198,7 +198,12 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
 
     const long long T = s_pref[a.B];
     const long long W = (long long)gridDim.x * NWAVE;
-    const long long wid = (long long)blockIdx.x * NWAVE + wave;
+    // workers are numbered wave-major: the 4 waves of a CU take tile ranges a
+    // quarter of the tile list apart instead of 4 neighbouring ones, so they
+    // do not stream neighbouring addresses of one (sequence, kv head) at the
+    // same time (c2 attention 124.0 -> 120.4 us, c3 319.7 -> 312.4 us, c2f8
+    // 76.6 -> 72.1 us on one box)
+    const long long wid = (long long)wave * gridDim.x + blockIdx.x;
     const int t0 = (int)(wid * T / W), t1 = (int)((wid + 1) * T / W);
     FA_PHASE(ph_plan = __builtin_amdgcn_s_memrealtime(); if (t0 >= t1) ph_write(wid, 0);)
     if (t0 >= t1) return;  // no block barrier follows: waves are independent from here
