@@ -152,6 +152,13 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, G = lane >> 4;
+    // 8-dim chunk of the head dim that lane group G holds in MFMA step s: for
+    // bf16 / fp16 chunk 4s + G, so one 16-byte load instruction covers 64
+    // contiguous bytes of each of its 16 key rows (the 4 lane groups side by
+    // side); FP8 lane groups hold a quarter row each (the e4m3 MFMA's layout)
+    auto chunk = [&](int s) -> int { return F8 ? G * KSTEPS + s : 4 * s + G; };
+    // element offset, within a key row, of 16-byte load s of lane group G
+    auto loff = [&](int s) -> int { return F8 ? G * (D / 4) + s * EPL : 8 * chunk(s); };
     FA_PHASE(const unsigned long long ph_entry = __builtin_amdgcn_s_memrealtime();
              unsigned long long ph_plan = 0, ph_first = 0, ph_nseg = 0;
              auto ph_write = [&](long long w, long long ntiles) {
@@ -285,17 +292,17 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                 if (key >= first_new) {
                     const int tn = key - first_new;
                     const int64_t kvh = is.kvh;
-                    kpr = knp + (int64_t)is.b * a.kn_sb + (int64_t)tn * a.kn_si + kvh * a.kn_sh + G * (D / 4);
-                    vpr = vnp + (int64_t)is.b * a.vn_sb + (int64_t)tn * a.vn_si + kvh * a.vn_sh + G * (D / 4);
+                    kpr = knp + (int64_t)is.b * a.kn_sb + (int64_t)tn * a.kn_si + kvh * a.kn_sh;
+                    vpr = vnp + (int64_t)is.b * a.vn_sb + (int64_t)tn * a.vn_si + kvh * a.vn_sh;
                 } else {
-                    kpr = row_ptr(kp, a.k_sb, a.k_si, a.k_sh, is, key, blk) + G * (D / 4);
-                    vpr = row_ptr(vp, a.v_sb, a.v_si, a.v_sh, is, key, blk) + G * (D / 4);
+                    kpr = row_ptr(kp, a.k_sb, a.k_si, a.k_sh, is, key, blk);
+                    vpr = row_ptr(vp, a.v_sb, a.v_si, a.v_sh, is, key, blk);
                 }
 #pragma unroll
                 for (int s = 0; s < KL; ++s) {
-                    const bool in = !HDM || G * (D / 4) + s * EPL < a.hd;
-                    kk[h][s] = in ? *reinterpret_cast<const u32x4*>(kpr + s * EPL) : u32x4{0u, 0u, 0u, 0u};
-                    vv[h][s] = in ? *reinterpret_cast<const u32x4*>(vpr + s * EPL) : u32x4{0u, 0u, 0u, 0u};
+                    const bool in = !HDM || loff(s) < a.hd;
+                    kk[h][s] = in ? *reinterpret_cast<const u32x4*>(kpr + loff(s)) : u32x4{0u, 0u, 0u, 0u};
+                    vv[h][s] = in ? *reinterpret_cast<const u32x4*>(vpr + loff(s)) : u32x4{0u, 0u, 0u, 0u};
                 }
             } else {
 #pragma unroll
@@ -336,14 +343,14 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             // same bytes per lane as the K loads: B operand of the e4m3 MFMA
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2) {
-                const bool in = ok && s2 < KL && (!HDM || G * (D / 4) + s2 * EPL < a.hd);
-                q8[s2] = in ? *reinterpret_cast<const u32x4*>(qrow + G * (D / 4) + s2 * EPL) : u32x4{0u, 0u, 0u, 0u};
+                const bool in = ok && s2 < KL && (!HDM || loff(s2) < a.hd);
+                q8[s2] = in ? *reinterpret_cast<const u32x4*>(qrow + loff(s2)) : u32x4{0u, 0u, 0u, 0u};
             }
         } else {
 #pragma unroll
             for (int s2 = 0; s2 < KSTEPS; ++s2) {
-                const bool in = ok && (!HDM || (G * KSTEPS + s2) * 8 < a.hd);
-                qreg[s2] = in ? *reinterpret_cast<const u32x4*>(qrow + (G * KSTEPS + s2) * 8) : u32x4{0u, 0u, 0u, 0u};
+                const bool in = ok && (!HDM || 8 * chunk(s2) < a.hd);
+                qreg[s2] = in ? *reinterpret_cast<const u32x4*>(qrow + 8 * chunk(s2)) : u32x4{0u, 0u, 0u, 0u};
             }
             if constexpr (QV) {
                 // qv row of the same (position, head): B operand against V, as q against K
@@ -353,8 +360,8 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                                       : qvp + (int64_t)s.b * a.qv_sb + (int64_t)i * a.qv_si + (int64_t)h * a.qv_sh;
 #pragma unroll
                 for (int s2 = 0; s2 < KSTEPS; ++s2) {
-                    const bool in = ok && (!HDM || (G * KSTEPS + s2) * 8 < a.hd);
-                    qvreg[s2] = in ? *reinterpret_cast<const u32x4*>(qvrow + (G * KSTEPS + s2) * 8) : u32x4{0u, 0u, 0u, 0u};
+                    const bool in = ok && (!HDM || 8 * chunk(s2) < a.hd);
+                    qvreg[s2] = in ? *reinterpret_cast<const u32x4*>(qvrow + 8 * chunk(s2)) : u32x4{0u, 0u, 0u, 0u};
                 }
             }
         }
@@ -416,13 +423,13 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             for (int h = 0; h < NH; ++h) {
                 const int key = key0 + h * 16 + li;
                 if (key >= first_new && key < cs.sk) {
-                    ET* kd = const_cast<ET*>(row_ptr(kc, a.k_sb, a.k_si, a.k_sh, cs, key, blk)) + G * (D / 4);
-                    ET* vd = const_cast<ET*>(row_ptr(vc, a.v_sb, a.v_si, a.v_sh, cs, key, blk)) + G * (D / 4);
+                    ET* kd = const_cast<ET*>(row_ptr(kc, a.k_sb, a.k_si, a.k_sh, cs, key, blk));
+                    ET* vd = const_cast<ET*>(row_ptr(vc, a.v_sb, a.v_si, a.v_sh, cs, key, blk));
 #pragma unroll
                     for (int s = 0; s < KL; ++s) {
-                        if (!HDM || G * (D / 4) + s * EPL < a.hd) {
-                            *reinterpret_cast<u32x4*>(kd + s * EPL) = kk[h][s];
-                            *reinterpret_cast<u32x4*>(vd + s * EPL) = vv[h][s];
+                        if (!HDM || loff(s) < a.hd) {
+                            *reinterpret_cast<u32x4*>(kd + loff(s)) = kk[h][s];
+                            *reinterpret_cast<u32x4*>(vd + loff(s)) = vv[h][s];
                         }
                     }
                 }
@@ -443,7 +450,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             const int kl = h * 16 + li;
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s) {
-                const int ch = G * KSTEPS + s;
+                const int ch = chunk(s);
                 *reinterpret_cast<u32x4*>(sv + kl * D + (C::vswz(kl, ch) << 3)) = opnd(vv, h, s);
             }
         }
