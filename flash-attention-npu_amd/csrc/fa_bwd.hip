@@ -55,9 +55,10 @@ struct BwCfg {
     static constexpr int CPQ = BQ * DCH / KNT;  // chunks per thread per q (and dout) tile
     // dQ kernel: 2 row blocks of 16 per wave up to head dim 128, so every
     // K / V operand read from LDS feeds twice the products (the kernel is
-    // bound by LDS reads; at 128 a few values spill, still 3053 -> 2762 us
-    // for the whole backward of B4 S4096 H32/8 causal); 8 waves and 64-key
-    // tiles up to 128, one wave per SIMD, 1 row block and 32-key tiles at 256
+    // bound by LDS reads: 3053 -> 2762 us for the whole backward of B4 S4096
+    // H32/8 causal; the BIAS instance spills a few values at 128); 8 waves
+    // and 64-key tiles up to 128, one wave per SIMD, 1 row block and 32-key
+    // tiles at 256
     static constexpr int QNW = HD > 128 ? 4 : 8;
     static constexpr int QNT = QNW * 64;
     static constexpr int RB = HD <= 128 ? 2 : 1;
@@ -189,8 +190,17 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
     using C = BwCfg<HD>;
     constexpr int D = C::D, DCH = C::DCH, KSTEPS = C::KSTEPS, DBLK = C::DBLK, BK = C::BK, BQ = C::BQ,
                   CPQ = C::CPQ, NT = C::KNT, KRB = C::KRB;
-    __shared__ __attribute__((aligned(16))) uint16_t s_q[2][BQ * D];
-    __shared__ __attribute__((aligned(16))) uint16_t s_do[2][BQ * D];
+    // The q and dout tiles (two buffers each) in one allocation. Head dim 128
+    // keeps them as 8-byte halves (split_addr128), and the dout tiles start 8
+    // bytes past a 512-byte boundary: no ds_read2 offset can then reach from a
+    // q half to a dout half, so the compiler cannot merge a lane's two reads
+    // into one ds_read2 (whose two addresses would share banks).
+    constexpr bool SPLIT = HD == 128;
+    constexpr int QT = BQ * D;                      // elements per tile
+    constexpr int DOFF = 2 * QT + (SPLIT ? 4 : 0);  // first dout element
+    __shared__ __attribute__((aligned(256))) uint16_t s_qdo[DOFF + 2 * QT];
+    auto sq = [&](int buf, int x) -> uint16_t* { return &s_qdo[buf * QT + x]; };
+    auto sdo = [&](int buf, int x) -> uint16_t* { return &s_qdo[DOFF + buf * QT + x]; };
     __shared__ __attribute__((aligned(16))) float s_lse[2][BQ];   // lse * log2(e); +inf for rows past the end
     __shared__ __attribute__((aligned(16))) float s_ds[2][BQ];    // dsum
     __shared__ __attribute__((aligned(16))) float s_sl[2][BQ];    // ALiBi slope of the row's head
@@ -205,15 +215,19 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
     });
 
     // LDS offsets: row reads (A operands) and transpose reads, both on the
-    // tv layout; staging stores
+    // tv layout (head dim 128: the split_addr128 layout of 8-byte halves, row
+    // reads as two ds_read_b64, offr[s] the first half, offr[s] ^ 64 the
+    // second); staging stores
     int offr[KSTEPS];
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) offr[s] = li * D + (tv(li, G * KSTEPS + s) << 3);
+    for (int s = 0; s < KSTEPS; ++s)
+        offr[s] = SPLIT ? split_addr128(li, G * KSTEPS + s, 0) : li * D + (tv(li, G * KSTEPS + s) << 3);
     const int r4 = li >> 2, c4 = li & 3;
     int offt[DBLK];
 #pragma unroll
     for (int db = 0; db < DBLK; ++db)
-        offt[db] = (4 * G + r4) * D + (tv(4 * G + r4, 2 * db + (c4 >> 1)) << 3) + (c4 & 1) * 4;
+        offt[db] = SPLIT ? split_addr128(4 * G + r4, 2 * db + (c4 >> 1), c4 & 1)
+                         : (4 * G + r4) * D + (tv(4 * G + r4, 2 * db + (c4 >> 1)) << 3) + (c4 & 1) * 4;
     const int dch = tid % DCH, rr0 = tid / DCH;
 
     const uint16_t* qp = static_cast<const uint16_t*>(a.q);
@@ -333,9 +347,17 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
 #pragma unroll
             for (int u = 0; u < CPQ; ++u) {
                 const int r = rr0 + u * (NT / DCH);
-                const int off = r * D + (tv(r, dch) << 3);
-                *reinterpret_cast<u32x4*>(&s_q[buf][off]) = qr[u];
-                *reinterpret_cast<u32x4*>(&s_do[buf][off]) = dr[u];
+                if constexpr (SPLIT) {
+                    const int o0 = split_addr128(r, dch, 0), o1 = o0 ^ 64;
+                    *reinterpret_cast<u32x2*>(sq(buf, o0)) = u32x2{qr[u][0], qr[u][1]};
+                    *reinterpret_cast<u32x2*>(sq(buf, o1)) = u32x2{qr[u][2], qr[u][3]};
+                    *reinterpret_cast<u32x2*>(sdo(buf, o0)) = u32x2{dr[u][0], dr[u][1]};
+                    *reinterpret_cast<u32x2*>(sdo(buf, o1)) = u32x2{dr[u][2], dr[u][3]};
+                } else {
+                    const int off = r * D + (tv(r, dch) << 3);
+                    *reinterpret_cast<u32x4*>(sq(buf, off)) = qr[u];
+                    *reinterpret_cast<u32x4*>(sdo(buf, off)) = dr[u];
+                }
             }
             if (tid < BQ) {
                 s_lse[buf][tid] = lr;
@@ -366,9 +388,29 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
             for (int s = 0; s < KSTEPS; ++s) {
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
-                    const int ro = (hh * 32 + t * 16) * D + offr[s];
-                    const u32x4 aq = *reinterpret_cast<const u32x4*>(&s_q[buf][ro]);
-                    const u32x4 ad = *reinterpret_cast<const u32x4*>(&s_do[buf][ro]);
+                    u32x4 aq, ad;
+                    if constexpr (SPLIT) {
+                        // LDS byte address of the first half; opaque to the
+                        // compiler, since reads 16 rows apart would otherwise
+                        // merge into ds_read2st64_b64, which reads both of a
+                        // lane's addresses (same banks) in one pass. The second
+                        // half is the other 128-byte plane (256-byte aligned
+                        // rows), the dout tile a fixed distance away.
+                        unsigned a0 = lds_addr(sq(buf, offr[s] + t * 16 * D));
+                        asm volatile("" : "+v"(a0));
+                        const unsigned a1 = a0 ^ 128u;
+                        constexpr unsigned DO = 2 * DOFF;  // bytes from a q element to its dout element
+                        const u32x2 q0 = lds_load_u32x2(a0 + hh * 32 * D * 2);
+                        const u32x2 q1 = lds_load_u32x2(a1 + hh * 32 * D * 2);
+                        const u32x2 d0 = lds_load_u32x2(a0 + DO + hh * 32 * D * 2);
+                        const u32x2 d1 = lds_load_u32x2(a1 + DO + hh * 32 * D * 2);
+                        aq = u32x4{q0[0], q0[1], q1[0], q1[1]};
+                        ad = u32x4{d0[0], d0[1], d1[0], d1[1]};
+                    } else {
+                        const int ro = (hh * 32 + t * 16) * D + offr[s];
+                        aq = *reinterpret_cast<const u32x4*>(sq(buf, ro));
+                        ad = *reinterpret_cast<const u32x4*>(sdo(buf, ro));
+                    }
 #pragma unroll
                     for (int rk = 0; rk < KRB; ++rk) {
                         sacc[rk][t] = mfma16x16x32<DT>(aq, kreg[rk][s], sacc[rk][t]);
@@ -428,10 +470,10 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
 #pragma unroll
             for (int db = 0; db < DBLK; ++db) {
                 const int o0 = offt[db] + (32 * hh) * D, o1 = offt[db] + (32 * hh + 16) * D;
-                const u32x2 dl = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_do[buf][o0]));
-                const u32x2 dh = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_do[buf][o1]));
-                const u32x2 ql = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_q[buf][o0]));
-                const u32x2 qh = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_q[buf][o1]));
+                const u32x2 dl = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)sdo(buf, o0)));
+                const u32x2 dh = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)sdo(buf, o1)));
+                const u32x2 ql = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)sq(buf, o0)));
+                const u32x2 qh = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)sq(buf, o1)));
                 const u32x4 dot = {dl[0], dl[1], dh[0], dh[1]}, qt = {ql[0], ql[1], qh[0], qh[1]};
 #pragma unroll
                 for (int rk = 0; rk < KRB; ++rk) {
@@ -508,8 +550,17 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
     using C = BwCfg<HD>;
     constexpr int D = C::D, DCH = C::DCH, KSTEPS = C::KSTEPS, DBLK = C::DBLK, RB = C::RB, BM = C::BM, BN = C::BN,
                   CPK = C::CPK, NT = C::QNT;
-    __shared__ __attribute__((aligned(16))) uint16_t s_k[2][BN * D];  // tv: row reads and transpose reads
-    __shared__ __attribute__((aligned(16))) uint16_t s_v[2][BN * D];  // tk: row reads
+    // K tiles (tv: row reads and transpose reads) and V tiles (tk: row reads),
+    // two buffers each, in one allocation. Head dim 128 keeps both as 8-byte
+    // halves (split_addr128) and starts the V tiles 8 bytes past a 512-byte
+    // boundary, so a lane's K and V reads cannot merge into one ds_read2
+    // (whose two addresses would share banks).
+    constexpr bool SPLIT = HD == 128;
+    constexpr int KT = BN * D;                      // elements per tile
+    constexpr int VOFF = 2 * KT + (SPLIT ? 4 : 0);  // first V element
+    __shared__ __attribute__((aligned(256))) uint16_t s_kv[VOFF + 2 * KT];
+    auto sk = [&](int buf, int x) -> uint16_t* { return &s_kv[buf * KT + x]; };
+    auto sv = [&](int buf, int x) -> uint16_t* { return &s_kv[VOFF + buf * KT + x]; };
     __shared__ int s_pref[bw::kMaxBatch + 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -519,17 +570,24 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
         return a.Hk * ((bb.rows + BM - 1) / BM);
     });
 
-    int offkr[KSTEPS], offvr[KSTEPS];
+    // row-read offsets of K and V (head dim 128: the first 8-byte half, the
+    // same for both tiles; the second half is ^ 64) and K^T transpose reads
+    int offkr[KSTEPS], offvr[SPLIT ? 1 : KSTEPS];
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
-        offkr[s] = li * D + (tv(li, G * KSTEPS + s) << 3);
-        offvr[s] = li * D + (tk(li, G * KSTEPS + s) << 3);
+        if constexpr (SPLIT) {
+            offkr[s] = split_addr128(li, G * KSTEPS + s, 0);
+        } else {
+            offkr[s] = li * D + (tv(li, G * KSTEPS + s) << 3);
+            offvr[s] = li * D + (tk(li, G * KSTEPS + s) << 3);
+        }
     }
     const int r4 = li >> 2, c4 = li & 3;
     int offt[DBLK];
 #pragma unroll
     for (int db = 0; db < DBLK; ++db)
-        offt[db] = (4 * G + r4) * D + (tv(4 * G + r4, 2 * db + (c4 >> 1)) << 3) + (c4 & 1) * 4;
+        offt[db] = SPLIT ? split_addr128(4 * G + r4, 2 * db + (c4 >> 1), c4 & 1)
+                         : (4 * G + r4) * D + (tv(4 * G + r4, 2 * db + (c4 >> 1)) << 3) + (c4 & 1) * 4;
     const int dch = tid % DCH, kk0 = tid / DCH;
 
     const uint16_t* qp = static_cast<const uint16_t*>(a.q);
@@ -623,8 +681,16 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
 #pragma unroll
             for (int u = 0; u < CPK; ++u) {
                 const int r = kk0 + u * (NT / DCH);
-                *reinterpret_cast<u32x4*>(&s_k[buf][r * D + (tv(r, dch) << 3)]) = kr[u];
-                *reinterpret_cast<u32x4*>(&s_v[buf][r * D + (tk(r, dch) << 3)]) = vr[u];
+                if constexpr (SPLIT) {
+                    const int o0 = split_addr128(r, dch, 0), o1 = o0 ^ 64;
+                    *reinterpret_cast<u32x2*>(sk(buf, o0)) = u32x2{kr[u][0], kr[u][1]};
+                    *reinterpret_cast<u32x2*>(sk(buf, o1)) = u32x2{kr[u][2], kr[u][3]};
+                    *reinterpret_cast<u32x2*>(sv(buf, o0)) = u32x2{vr[u][0], vr[u][1]};
+                    *reinterpret_cast<u32x2*>(sv(buf, o1)) = u32x2{vr[u][2], vr[u][3]};
+                } else {
+                    *reinterpret_cast<u32x4*>(sk(buf, r * D + (tv(r, dch) << 3))) = kr[u];
+                    *reinterpret_cast<u32x4*>(sv(buf, r * D + (tk(r, dch) << 3))) = vr[u];
+                }
             }
         };
 
@@ -645,8 +711,25 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
             for (int s = 0; s < KSTEPS; ++s) {
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
-                    const u32x4 ak = *reinterpret_cast<const u32x4*>(&s_k[buf][offkr[s] + (hh * 32 + kb * 16) * D]);
-                    const u32x4 av = *reinterpret_cast<const u32x4*>(&s_v[buf][offvr[s] + (hh * 32 + kb * 16) * D]);
+                    u32x4 ak, av;
+                    if constexpr (SPLIT) {
+                        // opaque LDS byte address of the first half (reads 16
+                        // rows apart would merge into ds_read2st64_b64, which
+                        // reads both of a lane's addresses in one pass)
+                        unsigned a0 = lds_addr(sk(buf, offkr[s] + kb * 16 * D));
+                        asm volatile("" : "+v"(a0));
+                        const unsigned a1 = a0 ^ 128u;
+                        constexpr unsigned VO = 2 * VOFF;  // bytes from a K element to its V element
+                        const u32x2 k0 = lds_load_u32x2(a0 + hh * 32 * D * 2);
+                        const u32x2 k1 = lds_load_u32x2(a1 + hh * 32 * D * 2);
+                        const u32x2 v0 = lds_load_u32x2(a0 + VO + hh * 32 * D * 2);
+                        const u32x2 v1 = lds_load_u32x2(a1 + VO + hh * 32 * D * 2);
+                        ak = u32x4{k0[0], k0[1], k1[0], k1[1]};
+                        av = u32x4{v0[0], v0[1], v1[0], v1[1]};
+                    } else {
+                        ak = *reinterpret_cast<const u32x4*>(sk(buf, offkr[s] + (hh * 32 + kb * 16) * D));
+                        av = *reinterpret_cast<const u32x4*>(sv(buf, offvr[s] + (hh * 32 + kb * 16) * D));
+                    }
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb) {
                         sacc[rb][kb] = mfma16x16x32<DT>(ak, qreg[rb][s], sacc[rb][kb]);
@@ -682,9 +765,9 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
 #pragma unroll
             for (int db = 0; db < DBLK; ++db) {
                 const u32x2 l2 = __builtin_bit_cast(
-                    u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_k[buf][offt[db] + (32 * hh) * D]));
+                    u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)sk(buf, offt[db] + (32 * hh) * D)));
                 const u32x2 h2 = __builtin_bit_cast(
-                    u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)&s_k[buf][offt[db] + (32 * hh + 16) * D]));
+                    u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)sk(buf, offt[db] + (32 * hh + 16) * D)));
                 const u32x4 kt = {l2[0], l2[1], h2[0], h2[1]};
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb) dqa[rb][db] = mfma16x16x32<DT>(kt, dsk[rb], dqa[rb][db]);

@@ -116,6 +116,30 @@ __device__ __forceinline__ int swz_b64(int r, int c) {
     return c ^ (((x & 3) << 1) | (x >> 2));
 }
 
+// 256-byte rows (head dim 128) kept as 8-byte halves, for tiles read both by
+// rows as 16x16x32 operands (two ds_read_b64 per operand: ds_read_b128 peaks
+// at half the LDS rate of ds_read_b64 on this part) and transposed with
+// ds_read_b64_tr_b16. Half h of 16-byte chunk c of row r sits in plane
+// h ^ ((c >> 2) & 1) (the two 128-byte halves of the row), slot
+// (c ^ pi(r)) & 15 with pi(r) = ((r & 7) << 1) | ((r >> 3) & 1). A row read
+// (lane li of group G: row li, chunk 4G + s, one half) puts groups 0 / 1 (2 /
+// 3) in different planes and 16 rows on 16 slots; a transpose read (rows
+// 4G + (li >> 2), chunks 2d, 2d + 1, half li & 1) puts the halves in different
+// planes and 8 rows x 2 chunks on 16 slots, since pi(0..7) and pi(8..15)
+// differ in their upper three bits. Either way 32 lanes cover the 64 banks.
+// Returns the element offset.
+// LDS byte address of a __shared__ element, and an 8-byte LDS load from one
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+    return (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ u32x2 lds_load_u32x2(unsigned a) {
+    return *(const __attribute__((address_space(3))) u32x2*)(size_t)a;
+}
+__device__ __forceinline__ int split_addr128(int r, int c, int h) {
+    const int pi = ((r & 7) << 1) | ((r >> 3) & 1);
+    return r * 128 + ((h ^ (c >> 2)) & 1) * 64 + ((c ^ pi) & 15) * 4;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
