@@ -408,6 +408,22 @@ def ceilings(torch, hip):
     res["gemm_bf16_tflops"] = round(2 * n ** 3 / t / 1e12, 1)
     res["note"] = "4 GiB bf16 copy (2 x 4 GiB moved), torch.sum of 4 GiB bf16, 8192^3 bf16 torch.matmul"
     torch.cuda.empty_cache()
+    # LDS read rates (bytes per shader clock per CU) of the kernels' access
+    # patterns, from the probe library build.py makes (csrc/probes/fa_lds_probe.hip)
+    probe = os.path.join(REPO, "flash-attention-npu_amd", "fa_mi355x", "lib", "libfa_lds_probe.so")
+    if os.path.exists(probe):
+        L = ctypes.CDLL(probe, mode=os.RTLD_LOCAL)
+        L.fa_lds_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+        names = ["b128_row", "b64_tr16", "b64", "2xb64_plane_split", "2xb64_naive", "read2st64_b64", "read2_b64"]
+        lds = {}
+        for pat, nm in enumerate(names):
+            for waves in (8, 16):
+                v = ctypes.c_double()
+                st = L.fa_lds_probe(pat, waves, ctypes.byref(v))
+                if st != 0:
+                    raise RuntimeError(f"fa_lds_probe({pat}, {waves}) failed: {st}")
+                lds[f"{nm}_w{waves}"] = round(v.value, 1)
+        res["lds_bytes_per_clk_per_cu"] = lds
     return res
 
 

@@ -77,9 +77,11 @@ def build(jobs=8, verbose=True):
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         futs = [ex.submit(_compile_hip, s) for s in HIP_SOURCES]
         pfut = ex.submit(_compile_hip, "fa_decode.hip", ("FA_DECODE_PHASES",), ".phases")
+        lfut = ex.submit(_compile_hip, os.path.join("probes", "fa_lds_probe.hip"))
         tfut = ex.submit(_run, torch_cmd)
         objs = [f.result() for f in futs]
         pobj = pfut.result()
+        lobj = lfut.result()
         tfut.result()
     core = os.path.join(LIBDIR, "libfa_mi355x.so")
     tmp = core + ".tmp"
@@ -91,6 +93,10 @@ def build(jobs=8, verbose=True):
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-Wl,-Bsymbolic", "-o", phases + ".tmp"]
          + pobjs)
     os.replace(phases + ".tmp", phases)
+    # the LDS read-rate probe behind the kernels' LDS layouts (bench.py --ceilings)
+    probe = os.path.join(LIBDIR, "libfa_lds_probe.so")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", probe + ".tmp", lobj])
+    os.replace(probe + ".tmp", probe)
     tlib = os.path.join(LIBDIR, "libfa_mi355x_torch.so")
     tmp = tlib + ".tmp"
     _run(["g++", "-shared", "-o", tmp, torch_obj, "-L", LIBDIR, "-lfa_mi355x", "-Wl,-rpath,$ORIGIN"] + ldflags)
