@@ -29,7 +29,10 @@ namespace dec {
 constexpr int NWAVE = 4;     // waves (workers) per workgroup
 constexpr int TABN = 256;    // paged: block ids staged per wave
 constexpr int MAXB = 2048;
-constexpr int MERGE_SPLIT = 4;  // merge workgroups per segment, each merging D / MERGE_SPLIT dims
+// merge workgroups per segment (each merges D / split dims): 4 where segments
+// carry 8 or more partials on average (c5 shapes: 9.5 us against 12.7 us with
+// 2), else 2 (c2: 8.1 against 9.1 us; one box, bench stage events)
+constexpr int MERGE_SPLIT_MANY = 4, MERGE_SPLIT_FEW = 2;
 }  // namespace dec
 
 #ifdef FA_DECODE_PHASES
@@ -590,8 +593,8 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     FA_PHASE(++ph_nseg; ph_write(wid, t1 - t0);)
 }
 
-// Merge of the partials a segment left in the decode kernel (4 workgroups per
-// segment, one per quarter of the head dim; a segment with no visible key
+// Merge of the partials a segment left in the decode kernel (DSPLIT workgroups
+// per segment, each on D / DSPLIT dims of the head; a segment with no visible key
 // gets out = 0, lse = +inf): per row, lse = M + ln(sum_j exp(lse_j - M)) and
 // O = sum_j exp(lse_j - lse) * O_j (the closed form of
 // CombineScale.hpp:150-194). The partial list of a segment [S, S+n) is known
@@ -602,12 +605,11 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
 // LDS. (Merging inside the decode kernel, by the last wave to finish a
 // segment, was measured 1.6x slower: every partial then needs a device-scope
 // fence, i.e. an L2 write-back across the 8 XCDs.)
-template <int DT, int D>
+template <int DT, int D, int DSPLIT>
 __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int workers) {
     using namespace dec;
     __shared__ __attribute__((aligned(16))) float s_acc[256][8];
     __shared__ float s_gm[256], s_gs[256];
-    constexpr int DSPLIT = MERGE_SPLIT;
     constexpr int CH = D / DSPLIT / 8;   // 8-dim chunks per row in one workgroup
     const int sig = blockIdx.x / DSPLIT, dsl = blockIdx.x % DSPLIT;
     const int b = sig / a.Hk, hk = sig % a.Hk;
@@ -768,16 +770,25 @@ hipError_t launch_decode(const FwdArgs& a, int dtype, int d, int grid, hipStream
     return hipGetLastError();
 }
 
+template <int DT, int DSPLIT>
+static void launch_decode_merge_s(const FwdArgs& a, int d, int w, hipStream_t stream) {
+    const int wgs = a.B * a.Hk * DSPLIT;  // DSPLIT workgroups per (sequence, kv head) segment
+    if (d == 64) hipLaunchKernelGGL((fa_decode_merge_kernel<DT, 64, DSPLIT>), dim3(wgs), dim3(256), 0, stream, a, w);
+    else hipLaunchKernelGGL((fa_decode_merge_kernel<DT, 128, DSPLIT>), dim3(wgs), dim3(256), 0, stream, a, w);
+}
+
 hipError_t launch_decode_merge(const FwdArgs& a, int dtype, int d, int grid, hipStream_t stream) {
     if (d != 64 && d != 128) return hipErrorInvalidValue;
-    const int segs = a.B * a.Hk * dec::MERGE_SPLIT;  // workgroups: MERGE_SPLIT per (sequence, kv head) segment
     const int w = grid * dec::NWAVE;
-    if (dtype == DT_BF16 || dtype == DT_FP8) {  // FP8 inputs give a bf16 output
-        if (d == 64) hipLaunchKernelGGL((fa_decode_merge_kernel<DT_BF16, 64>), dim3(segs), dim3(256), 0, stream, a, w);
-        else hipLaunchKernelGGL((fa_decode_merge_kernel<DT_BF16, 128>), dim3(segs), dim3(256), 0, stream, a, w);
+    // partials per segment on average (every worker leaves at most 2)
+    const bool many = (int64_t)w >= 8LL * a.B * a.Hk;
+    const int odt = (dtype == DT_BF16 || dtype == DT_FP8) ? DT_BF16 : DT_FP16;  // FP8 inputs give a bf16 output
+    if (odt == DT_BF16) {
+        if (many) launch_decode_merge_s<DT_BF16, dec::MERGE_SPLIT_MANY>(a, d, w, stream);
+        else launch_decode_merge_s<DT_BF16, dec::MERGE_SPLIT_FEW>(a, d, w, stream);
     } else {
-        if (d == 64) hipLaunchKernelGGL((fa_decode_merge_kernel<DT_FP16, 64>), dim3(segs), dim3(256), 0, stream, a, w);
-        else hipLaunchKernelGGL((fa_decode_merge_kernel<DT_FP16, 128>), dim3(segs), dim3(256), 0, stream, a, w);
+        if (many) launch_decode_merge_s<DT_FP16, dec::MERGE_SPLIT_MANY>(a, d, w, stream);
+        else launch_decode_merge_s<DT_FP16, dec::MERGE_SPLIT_FEW>(a, d, w, stream);
     }
     return hipGetLastError();
 }
