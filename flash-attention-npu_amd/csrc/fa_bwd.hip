@@ -457,7 +457,8 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
                             }
                             pv = vis ? pv : 0.f;
                         }
-                        float dsv = pv * (pacc[rk][t][e] - d4[t][e]) * a.scale;
+                        // dS without the softmax scale, which is applied to dK once at the end
+                        float dsv = pv * (pacc[rk][t][e] - d4[t][e]);
                         if constexpr (BIAS) dsv *= 1.f - th * th;
                         p[t][e] = pv;
                         ds[t][e] = dsv;
@@ -529,8 +530,8 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
 #pragma unroll
                 for (int db = 0; db < DBLK; ++db) {
                     if (16 * db + 4 * G >= a.hd) continue;
-                    uint16_t k4[4] = {f32_to_16<DT>(dka[rk][db][0]), f32_to_16<DT>(dka[rk][db][1]),
-                                      f32_to_16<DT>(dka[rk][db][2]), f32_to_16<DT>(dka[rk][db][3])};
+                    const f32x4 kk = dka[rk][db] * a.scale;
+                    uint16_t k4[4] = {f32_to_16<DT>(kk[0]), f32_to_16<DT>(kk[1]), f32_to_16<DT>(kk[2]), f32_to_16<DT>(kk[3])};
                     uint16_t v4[4] = {f32_to_16<DT>(dva[rk][db][0]), f32_to_16<DT>(dva[rk][db][1]),
                                       f32_to_16<DT>(dva[rk][db][2]), f32_to_16<DT>(dva[rk][db][3])};
                     *reinterpret_cast<u32x2*>(dkp + 16 * db + 4 * G) = __builtin_bit_cast(u32x2, k4);
@@ -755,7 +756,8 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
                             const bool vis = j < k_hi && j >= rlo[rb] && j <= rhi[rb];
                             pv = vis ? pv : 0.f;
                         }
-                        float d = pv * (pacc[rb][kb][e] - dsv[rb]) * a.scale;
+                        // dS without the softmax scale, which is applied to dQ once at the end
+                        float d = pv * (pacc[rb][kb][e] - dsv[rb]);
                         if constexpr (BIAS) d *= 1.f - th * th;
                         ds[kb][e] = d;
                     }
@@ -811,8 +813,8 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
 #pragma unroll
             for (int db = 0; db < DBLK; ++db) {
                 if (16 * db + 4 * G >= a.hd) continue;
-                uint16_t q4[4] = {f32_to_16<DT>(dqa[rb][db][0]), f32_to_16<DT>(dqa[rb][db][1]),
-                                  f32_to_16<DT>(dqa[rb][db][2]), f32_to_16<DT>(dqa[rb][db][3])};
+                const f32x4 qq = dqa[rb][db] * a.scale;
+                uint16_t q4[4] = {f32_to_16<DT>(qq[0]), f32_to_16<DT>(qq[1]), f32_to_16<DT>(qq[2]), f32_to_16<DT>(qq[3])};
                 *reinterpret_cast<u32x2*>(row + 16 * db + 4 * G) = __builtin_bit_cast(u32x2, q4);
             }
         }
