@@ -381,6 +381,15 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         for (int db = 0; db < DBLK; ++db) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
     };
 
+    // The partial of the worker's first segment, when the worker goes on to
+    // other segments, is held in registers and stored when the worker ends:
+    // no partial store then enters the memory queue while the worker streams
+    // (c3 attention ~314 -> ~309 us with all partial stores removed, timing-only
+    // variant; the first segment's is the one mid-stream).
+    f32x4 dpo[DBLK];
+    float dlse = 0.f;
+    int64_t dprow = -1;
+
     auto end_seg = [&](const DecSeg& s) {
         const float lrow = wave_sum16x4(l_run);
         const bool nonempty = lrow > 0.f;
@@ -408,10 +417,18 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         } else {
             const int slot = (s.S <= t0) ? 0 : 1;  // first segment of this worker, else its last
             const int64_t prow = (wid * 2 + slot) * 16 + li;
+            const float plse = nonempty ? (m_run + fast_log2(lrow)) * kLn2 : -INFINITY;
+            if (slot == 0 && s.S + s.n < t1) {  // more segments follow: store at the end
+#pragma unroll
+                for (int db = 0; db < DBLK; ++db) dpo[db] = oacc[db] * inv;
+                dlse = plse;
+                dprow = prow;
+                return;
+            }
 #pragma unroll
             for (int db = 0; db < DBLK; ++db)
                 *reinterpret_cast<f32x4*>(a.part_o + prow * D + 16 * db + 4 * G) = oacc[db] * inv;
-            if (G == 0) a.part_lse[prow] = nonempty ? (m_run + fast_log2(lrow)) * kLn2 : -INFINITY;
+            if (G == 0) a.part_lse[prow] = plse;
         }
     };
 
@@ -590,6 +607,11 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         }
     }
     end_seg(cs);
+    if (dprow >= 0) {
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db) *reinterpret_cast<f32x4*>(a.part_o + dprow * D + 16 * db + 4 * G) = dpo[db];
+        if (G == 0) a.part_lse[dprow] = dlse;
+    }
     FA_PHASE(++ph_nseg; ph_write(wid, t1 - t0);)
 }
 
