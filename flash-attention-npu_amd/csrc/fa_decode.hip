@@ -424,6 +424,22 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     f32x4 dpo[DBLK];
     float dlse = 0.f;
     int64_t dprow = -1;
+    // Likewise the output of the latest whole segment: stored when the next
+    // whole segment ends or when the worker ends.
+    u32x2 hwo[DBLK];
+    float hwlse = 0.f;
+    uint16_t* hworow = nullptr;
+    int64_t hwoff = -1;
+    auto flush_whole = [&]() {
+        if (hworow == nullptr) return;
+#pragma unroll
+        for (int db = 0; db < DBLK; ++db) {
+            if (HDM && 16 * db + 4 * G >= a.hd) continue;
+            *reinterpret_cast<u32x2*>(hworow + 16 * db + 4 * G) = hwo[db];
+        }
+        if (G == 0) a.lse[hwoff] = hwlse;
+        hworow = nullptr;
+    };
 
     auto end_seg = [&](const DecSeg& s) {
         const float lrow = wave_sum16x4(l_run);
@@ -437,18 +453,17 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             uint16_t* orow = a.cu_seqlens_q
                                  ? op + ((int64_t)a.cu_seqlens_q[s.b] + i) * a.o_si + (int64_t)h * a.o_sh
                                  : op + (int64_t)s.b * a.o_sb + (int64_t)i * a.o_si + (int64_t)h * a.o_sh;
+            flush_whole();
 #pragma unroll
             for (int db = 0; db < DBLK; ++db) {
-                if (HDM && 16 * db + 4 * G >= a.hd) continue;
                 f32x4 o = oacc[db] * inv;
                 uint16_t h4[4] = {f32_to_16<DT>(o[0]), f32_to_16<DT>(o[1]), f32_to_16<DT>(o[2]), f32_to_16<DT>(o[3])};
-                *reinterpret_cast<u32x2*>(orow + 16 * db + 4 * G) = __builtin_bit_cast(u32x2, h4);
+                hwo[db] = __builtin_bit_cast(u32x2, h4);
             }
-            if (G == 0) {
-                const int64_t off = a.cu_seqlens_q ? (int64_t)h * a.lse_sh + a.cu_seqlens_q[s.b] + i
-                                                   : (int64_t)s.b * a.lse_sb + (int64_t)h * a.lse_sh + i;
-                a.lse[off] = nonempty ? (m_run + fast_log2(lrow)) * kLn2 : INFINITY;
-            }
+            hworow = orow;
+            hwoff = a.cu_seqlens_q ? (int64_t)h * a.lse_sh + a.cu_seqlens_q[s.b] + i
+                                   : (int64_t)s.b * a.lse_sb + (int64_t)h * a.lse_sh + i;
+            hwlse = nonempty ? (m_run + fast_log2(lrow)) * kLn2 : INFINITY;
         } else {
             const int slot = (s.S <= t0) ? 0 : 1;  // first segment of this worker, else its last
             const int64_t prow = (wid * 2 + slot) * 16 + li;
@@ -642,6 +657,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         }
     }
     end_seg(cs);
+    flush_whole();
     if (dprow >= 0) {
 #pragma unroll
         for (int db = 0; db < DBLK; ++db) *reinterpret_cast<f32x4*>(a.part_o + dprow * D + 16 * db + 4 * G) = dpo[db];
