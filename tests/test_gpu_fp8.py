@@ -130,6 +130,38 @@ def test_fp8_paged_decode_gqa(page):
     check(out, lse, ro, rl, vmax=float(vd.max()))
 
 
+def test_fp8_paged_decode_many_segments():
+    # config-3 regime with fp8: 512 (sequence, kv head) segments and >= 16
+    # 64-key tiles per wave worker, so the decode split counts segments
+    import flash_attn_npu_v3 as fa3
+    print("case fp8 paged decode many segments", flush=True)
+    g = torch.Generator().manual_seed(36)
+    B, Sq, H, Hk, D, page = 64, 1, 64, 8, 128, 256
+    rng = np.random.default_rng(36)
+    L = torch.tensor(np.round(np.exp(rng.uniform(np.log(512), np.log(8192), size=B))).astype(np.int32))
+    assert B * Hk * int(L.float().mean()) // 64 >= 16 * 1024
+    need = [(int(l) + page - 1) // page for l in L]
+    mb = max(need)
+    nblocks = sum(need) + 2
+    perm = torch.randperm(nblocks, generator=g)
+    bt = torch.zeros((B, mb), dtype=torch.int32)
+    o = 0
+    for b in range(B):
+        bt[b, :need[b]] = perm[o:o + need[b]]
+        o += need[b]
+    kc, vc = fp8((nblocks, page, Hk, D), g), fp8((nblocks, page, Hk, D), g)
+    q = fp8((B, Sq, H, D), g)
+    qd, kd, vd = descales(B, Hk, g)
+    out, lse, *_ = fa3.flash_attn_with_kvcache(q.to(DEV), kc.to(DEV), vc.to(DEV), cache_seqlens=L.to(DEV),
+                                               page_table=bt.to(DEV), q_descale=qd.to(DEV), k_descale=kd.to(DEV),
+                                               v_descale=vd.to(DEV), causal=True, return_softmax_lse=True)
+    kx = u8(kc)[bt.numpy()].reshape(B, mb * page, Hk, D)
+    vx = u8(vc)[bt.numpy()].reshape(B, mb * page, Hk, D)
+    ro, rl = orc.attention_fp8(u8(q), kx, vx, scale=D ** -0.5, q_descale=qd.numpy(), k_descale=kd.numpy(),
+                               v_descale=vd.numpy(), causal=True, seqlens_k=L.numpy(), nthreads=NT)
+    check(out, lse, ro, rl, vmax=float(vd.max()))
+
+
 @pytest.mark.parametrize("D,causal,window,softcap", [(64, True, (-1, -1), 0.0), (96, True, (-1, -1), 0.0),
                                                      (128, True, (-1, -1), 0.0), (128, False, (100, 20), 0.0),
                                                      (256, True, (-1, -1), 0.0), (128, True, (-1, -1), 30.0)])

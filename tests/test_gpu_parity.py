@@ -358,6 +358,18 @@ def test_decode_large_paged_uneven():
     run_kvcache(12, 1, 64, 8, 128, torch.bfloat16, 0, seqlens, s_new=1, page=256, causal=True, seed=32)
 
 
+def test_decode_many_segments_cost_split():
+    # 64 x 8 = 512 (sequence, kv head) segments over 1024 wave workers with at
+    # least 16 tiles each: the regime of BASELINE config 3, where the decode
+    # split counts every segment as one extra tile and a worker's first
+    # partial and latest whole output are held until it ends
+    print("case decode many segments (split by cost)", flush=True)
+    rng = np.random.default_rng(35)
+    seqlens = np.round(np.exp(rng.uniform(np.log(512), np.log(8192), size=64))).astype(np.int64)
+    assert 64 * 8 * int(np.mean(seqlens)) // 32 >= 16 * 1024
+    run_kvcache(64, 1, 64, 8, 128, torch.bfloat16, 0, seqlens, s_new=1, page=256, causal=True, seed=35)
+
+
 def test_decode_one_long_sequence():
     # one (sequence, kv head) segment spans every wave worker: the merge combines ~1024 partials
     print("case decode one long sequence", flush=True)
