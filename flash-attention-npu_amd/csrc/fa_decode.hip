@@ -714,8 +714,8 @@ __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int wor
     // one of this batch, else the last one of the nearest batch with tiles
     bool first_slot1 = false;
     if (per > 0 && S > 0) {
-        long long jp = sig - 1;
-        if (hk == 0) {
+        long long jp = sig - 1;  // only its cost matters, and only when ovh > 0
+        if (hk == 0 && ovh > 0) {
             int bp = b - 1;
             while (bp > 0 && a.sched[bp + 1] == a.sched[bp]) --bp;
             jp = (long long)bp * a.Hk + a.Hk - 1;
