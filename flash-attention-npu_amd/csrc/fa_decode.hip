@@ -21,6 +21,7 @@
 //     fa_decode_merge_kernel (the kernel boundary orders the partials).
 #include "fa_common.h"
 #include "fa_kernel_args.h"
+#include "fa_decode_split.h"
 
 #include <type_traits>
 
@@ -34,21 +35,6 @@ constexpr int MAXB = 2048;
 // 2), else 2 (c2: 8.1 against 9.1 us; one box, bench stage events)
 constexpr int MERGE_SPLIT_MANY = 4, MERGE_SPLIT_FEW = 2;
 
-// Static split by cost: a worker that moves to another (sequence, kv head)
-// segment pays about a tile's time for it (the q reload and the store of the
-// finished segment). Where workers cross many segments (at least half a
-// segment per worker: B * Hk >= W / 2) and own at least 16 tiles each, every
-// segment counts kSegCost tiles more, so workers crossing many short
-// segments get fewer tiles. Tile t of segment j (j = b * Hk + hk) costs
-// t + ovh * j, and worker w owns the tiles whose cost lies in
-// [w * CT / W, (w + 1) * CT / W), CT = T + ovh * B * Hk. (Measured, one box,
-// three runs each: c3 305.7 -> 303.8 us, c3f8 178.5 -> 175.3 us; c2, with a
-// quarter segment per worker, was 2 us slower with it and keeps the plain
-// split.)
-constexpr long long kSegCost = 1;
-__device__ __forceinline__ long long seg_ovh(long long T, long long W, long long segs) {
-    return (T >= 16 * W && 2 * segs >= W) ? kSegCost : 0;
-}
 }  // namespace dec
 
 #ifdef FA_DECODE_PHASES
@@ -230,26 +216,11 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     // same time (c2 attention 124.0 -> 120.4 us, c3 319.7 -> 312.4 us, c2f8
     // 76.6 -> 72.1 us on one box)
     const long long wid = (long long)wave * gridDim.x + blockIdx.x;
+    // tiles [t0, t1) of this worker: the split by cost of fa_decode_split.h
     const long long ovh = seg_ovh(T, W, (long long)a.B * a.Hk);
-    const long long CT = T + ovh * a.B * a.Hk;  // total cost
-    // first tile whose cost is >= c (segment starts in cost space: batch b's
-    // first at s_pref[b] + ovh * b * Hk, then one every nt_b + ovh)
-    auto tfirst = [&](long long c) -> int {
-        if (ovh == 0) return (int)c;
-        if (c >= CT) return (int)T;
-        int bl = 0, bh = a.B;
-        while (bh - bl > 1) {
-            const int mid = (bl + bh) >> 1;
-            if (s_pref[mid] + ovh * mid * a.Hk <= c) bl = mid;
-            else bh = mid;
-        }
-        const long long cb = s_pref[bl] + ovh * bl * a.Hk;
-        const long long nt = (s_pref[bl + 1] - s_pref[bl]) / a.Hk;
-        const long long hk = min((c - cb) / (nt + ovh), (long long)a.Hk - 1);
-        const long long off = c - cb - hk * (nt + ovh);
-        return (int)(s_pref[bl] + hk * nt + min(off, nt));
-    };
-    const int t0 = tfirst(wid * CT / W), t1 = tfirst((wid + 1) * CT / W);
+    const long long CT = split_total(T, ovh, a.B, a.Hk);
+    const int t0 = split_tfirst(wid * CT / W, s_pref, a.B, a.Hk, ovh, T, CT);
+    const int t1 = split_tfirst((wid + 1) * CT / W, s_pref, a.B, a.Hk, ovh, T, CT);
     FA_PHASE(ph_plan = __builtin_amdgcn_s_memrealtime(); if (t0 >= t1) ph_write(wid, 0);)
     if (t0 >= t1) return;  // no block barrier follows: waves are independent from here
 
@@ -696,12 +667,11 @@ __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int wor
     const long long S = a.sched[b] + (long long)hk * per;
     const long long W = workers;
     const int tid = threadIdx.x;
-    // the split of the decode kernel (dec::seg_ovh): tile t of segment j costs
-    // t + ovh * j, and worker w owns the costs [w * CT / W, (w + 1) * CT / W)
+    // the split of the decode kernel (fa_decode_split.h): tile t of segment j
+    // costs t + ovh * j, and worker w owns the costs [w * CT / W, (w + 1) * CT / W)
     const long long ovh = seg_ovh(T, W, (long long)a.B * a.Hk);
-    const long long CT = T + ovh * a.B * a.Hk;  // total cost
-    auto owner_c = [&](long long c) { return ((c + 1) * W - 1) / CT; };
-    auto owner = [&](long long t) { return owner_c(t + ovh * sig); };  // t in this segment
+    const long long CT = split_total(T, ovh, a.B, a.Hk);
+    auto owner = [&](long long t) { return split_owner(t + ovh * sig, W, CT); };  // t in this segment
     long long wf = 0;
     int n = 0;
     if (per > 0) {
@@ -714,13 +684,9 @@ __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int wor
     // one of this batch, else the last one of the nearest batch with tiles
     bool first_slot1 = false;
     if (per > 0 && S > 0) {
-        long long jp = sig - 1;  // only its cost matters, and only when ovh > 0
-        if (hk == 0 && ovh > 0) {
-            int bp = b - 1;
-            while (bp > 0 && a.sched[bp + 1] == a.sched[bp]) --bp;
-            jp = (long long)bp * a.Hk + a.Hk - 1;
-        }
-        first_slot1 = owner_c(S - 1 + ovh * jp) == wf;
+        // that tile's segment only matters through its cost, so only when ovh > 0
+        const long long jp = ovh > 0 ? split_prev_segment(b, hk, a.Hk, a.sched) : 0;
+        first_slot1 = split_owner(S - 1 + ovh * jp, W, CT) == wf;
     }
     // partial j of this segment -> its first partial row
     auto prow0 = [&](int j) -> long long {

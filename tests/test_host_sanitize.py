@@ -28,3 +28,18 @@ def test_c_abi_host_code_under_asan_ubsan(tmp_path):
     r = subprocess.run([str(exe)], capture_output=True, text=True, env=env, timeout=300)
     assert r.returncode == 0, (r.stdout + r.stderr)[-4000:]
     assert "0 failures" in r.stdout, r.stdout
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+def test_decode_split_against_brute_force(tmp_path):
+    """The decode kernel's tile split and the merge's owner / slot lookups
+    (csrc/fa_decode_split.h, host and device code alike) against brute force,
+    under ASan / UBSan."""
+    exe = tmp_path / "split_check"
+    cmd = ["g++", "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+           "-I", CSRC, os.path.join(REPO, "tests", "host", "fa_decode_split_check.cpp"), "-o", str(exe)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-4000:]
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, (r.stdout + r.stderr)[-4000:]
+    assert " 0 failures" in r.stdout, r.stdout
