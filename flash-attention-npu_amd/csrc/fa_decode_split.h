@@ -49,19 +49,23 @@ FA_SPLIT_FN int split_tfirst(long long c, const int* pref, int B, int Hk, long l
                              long long CT) {
     if (ovh == 0) return (int)c;
     if (c >= CT) return (int)T;
+    // 32-bit arithmetic (a 64-bit division is a long instruction sequence on
+    // the GPU): T counts 8-16 KB tiles, so CT = T + ovh * B * Hk stays far
+    // below 2^31 for any cache that fits in memory
+    const int ci = (int)c, ov = (int)ovh;
     int bl = 0, bh = B;
     while (bh - bl > 1) {
         const int mid = (bl + bh) >> 1;
-        if (pref[mid] + ovh * mid * Hk <= c) bl = mid;
+        if (pref[mid] + ov * mid * Hk <= ci) bl = mid;
         else bh = mid;
     }
-    const long long cb = pref[bl] + ovh * bl * Hk;
-    const long long nt = (pref[bl + 1] - pref[bl]) / Hk;
-    long long hk = (c - cb) / (nt + ovh);
+    const int cb = pref[bl] + ov * bl * Hk;
+    const int nt = (pref[bl + 1] - pref[bl]) / Hk;
+    int hk = (int)((unsigned)(ci - cb) / (unsigned)(nt + ov));
     if (hk > Hk - 1) hk = Hk - 1;
-    long long off = c - cb - hk * (nt + ovh);
+    int off = ci - cb - hk * (nt + ov);
     if (off > nt) off = nt;
-    return (int)(pref[bl] + hk * nt + off);
+    return pref[bl] + hk * nt + off;
 }
 
 // the worker whose cost range holds cost c (0 <= c < CT)
