@@ -43,9 +43,21 @@ def _run(cmd):
     return out
 
 
+# Per-source LLVM scheduler choice. The prefill kernels (fa_fwd.hip) are
+# scheduled with max-memory-clause: the c4 prefill kernel measured 919-922 us
+# against 928-929 us with the default strategy (same box, alternating runs;
+# 954 vs 962 us on a second box), max-ilp 977 us, iterative-ilp 1021 us.
+# Decode and the backward are faster with the default (max-memory-clause / max-ilp
+# were +1-2 % on c2 / c3 decode and +6 % on the backward).
+SRC_FLAGS = {
+    "fa_fwd.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"],
+}
+
+
 def _compile_hip(src, defines=(), tag=""):
     obj = os.path.join(OBJDIR, os.path.basename(src) + tag + ".o")
-    cmd = [HIPCC] + HIPFLAGS + [f"-D{d}" for d in defines] + ["-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = ([HIPCC] + HIPFLAGS + SRC_FLAGS.get(os.path.basename(src), []) + [f"-D{d}" for d in defines]
+           + ["-c", os.path.join(CSRC, src), "-o", obj])
     _run(cmd)
     return obj
 
