@@ -11,7 +11,10 @@ the CPU-runnable parity anchor and is not a bench line.
 Every call goes through the C ABI (libfa_mi355x.so via ctypes); PyTorch only
 allocates device memory and supplies the stream. Kernel durations come from
 HIP events recorded by the library at stage boundaries (fa_fwd_params.
-stage_events) on the stream the kernels run on. Caches are rotated between
+stage_events) on the stream the kernels run on. Each stage also carries the
+cost of its event packets (a few us; `event_pair_us` where a config has no
+append kernel and the append stage is empty), so stage times are upper bounds
+of the kernel durations that a rocprofv3 kernel trace gives. Caches are rotated between
 copies so reads are not served by the 256 MB Infinity Cache. Each config
 gets W untimed warmup calls, then untimed calls for about 150 ms more (the
 shader clock ramps up after the idle gap spent building the config's inputs),
@@ -626,6 +629,13 @@ def main():
         t = time_case(c, hip, torch, args.steps, args.warmup)
         r = dict(t)
         r["workload"] = c["work_desc"]
+        if name != "c4":
+            # only c4 launches an append kernel (kv_prep); c2 / c3 / c2f8 / c3f8
+            # append their one token inside the decode kernel and c5 appends
+            # nothing, so their append stage times only the two event packets.
+            # That figure is the event cost carried by attn_us and combine_us too.
+            r["append_us"] = None
+            r["event_pair_us"] = t["append_us"]
         if c["bound"] == "hbm":
             r["bytes_per_call"] = c["bytes"]
             r["tbps_call"] = c["bytes"] / (t["us_per_call"] * 1e-6) / 1e12
