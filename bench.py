@@ -20,6 +20,11 @@ gets W untimed warmup calls, then untimed calls for about 150 ms more (the
 shader clock ramps up after the idle gap spent building the config's inputs),
 then exactly K timed calls.
 
+Each of configs 2-5 also carries a `parity` block: one more call on the
+benchmarked inputs, compared with the oracle's result on the cpu_baseline
+sample (out max-abs, LSE relative error, the cache after the append bit for
+bit); the headline's is repeated at the top level.
+
 `configs` also carries "bwd", the backward of a dense causal training shape,
 and "c2f8" / "c3f8", configs 2 and 3 with q, the caches and the new k/v in
 float8_e4m3fn (bf16 out); none of these is a BASELINE config.
@@ -322,7 +327,9 @@ def cpu_baseline(c, torch):
     on a bounded sample of the config's own inputs, in the config's unit:
       c2 / c3: the first sequences (all heads), TB/s of the same algorithmic bytes;
       c4: one (batch, kv head) slice (its 4 query heads, rotary and append), TFLOP/s;
-      c5: the whole config, TB/s."""
+      c5: the whole config, TB/s.
+    Returns (baseline, ref): ref holds the oracle's out / LSE / caches after the
+    append for that sample, which parity() compares with the GPU's."""
     import numpy as np
     from oracle import fa_oracle as orc
     nt = _cpu_threads()
@@ -345,35 +352,97 @@ def cpu_baseline(c, torch):
             kh, vh = bits(kc[used.to(kc.device).long()]), bits(vc[used.to(vc.device).long()])
             bth = remap[rows.long()].numpy()
         Ls = L[:nb]
-        dt, reps = _timed(lambda: orc.kvcache_forward(qh, kh, vh, dtype=orc.BF16, cache_seqlens=Ls.numpy(), k=knh,
-                                                      v=vnh, block_table=bth, causal=True, nthreads=nt))
+        res = {}
+
+        def run():
+            res["r"] = orc.kvcache_forward(qh, kh, vh, dtype=orc.BF16, cache_seqlens=Ls.numpy(), k=knh, v=vnh,
+                                           block_table=bth, causal=True, nthreads=nt)
+        dt, reps = _timed(run)
         nbytes = 2 * int((Ls + 1).sum()) * Hk * D * 2 + 2 * nb * H * D * 2 + 4 * nb * H + 2 * 2 * nb * Hk * D * 2
-        return {"value": round(nbytes / dt / 1e12, 6), "unit": "TB/s", "cores": nt, "host_cores": os.cpu_count(),
-                "kind": "port", "sample": f"config {name[1]}, sequences 0..{nb - 1} of {c['B']} (all {H} q heads), "
-                f"oracle/fa_oracle.c on {nt} OpenMP threads, {reps} reps, {dt * 1e3:.1f} ms/rep"}
+        sample = f"config {name[1]}, sequences 0..{nb - 1} of {c['B']} (all {H} q heads)"
+        ro, rl, rk, rv = res["r"]
+        sel_kv = (lambda t: t[:nb]) if bt is None else (lambda t: t[used.to(t.device).long()])
+        ref = {"out": ro, "lse": rl, "k": rk, "v": rv, "sel_q": lambda t: t[:nb], "sel_kv": sel_kv,
+               "sample": sample + ("" if bt is None else ", the cache pages they use")}
+        return ({"value": round(nbytes / dt / 1e12, 6), "unit": "TB/s", "cores": nt, "host_cores": os.cpu_count(),
+                 "kind": "port", "sample": f"{sample}, oracle/fa_oracle.c on {nt} OpenMP threads, {reps} reps, "
+                 f"{dt * 1e3:.1f} ms/rep"}, ref)
     if name == "c4":
         g = H // Hk
         qh = bits(q[0:1, :, 0:g])
         kh, vh = bits(kc[0:1, :, 0:1]), bits(vc[0:1, :, 0:1])
         knh, vnh = bits(kn[0:1, :, 0:1]), bits(vn[0:1, :, 0:1])
         ch, sh = bits(cos), bits(sin)
-        dt, reps = _timed(lambda: orc.kvcache_forward(qh, kh, vh, dtype=orc.BF16, cache_seqlens=L[0:1].numpy(), k=knh,
-                                                      v=vnh, rotary_cos=ch, rotary_sin=sh, rotary_interleaved=False,
-                                                      causal=True, nthreads=nt))
+        res = {}
+
+        def run():
+            res["r"] = orc.kvcache_forward(qh, kh, vh, dtype=orc.BF16, cache_seqlens=L[0:1].numpy(), k=knh, v=vnh,
+                                           rotary_cos=ch, rotary_sin=sh, rotary_interleaved=False, causal=True,
+                                           nthreads=nt)
+        dt, reps = _timed(run)
         flops = c["flops"] / (c["B"] * H) * g
-        return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": nt, "host_cores": os.cpu_count(),
-                "kind": "port", "sample": f"config 4, batch 0 x kv head 0 (q heads 0..{g - 1}): 1/{c['B'] * Hk} of "
-                f"the work, oracle/fa_oracle.c on {nt} OpenMP threads, {reps} reps, {dt * 1e3:.0f} ms/rep"}
+        sample = f"config 4, batch 0 x kv head 0 (q heads 0..{g - 1}): 1/{c['B'] * Hk} of the work"
+        ro, rl, rk, rv = res["r"]
+        ref = {"out": ro, "lse": rl, "k": rk, "v": rv, "sel_q": lambda t: t[0:1, :, 0:g] if t.dim() == 4 else t[0:1, 0:g],
+               "sel_kv": lambda t: t[0:1, :, 0:1], "sample": sample + ", its whole cache after the append"}
+        return ({"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": nt, "host_cores": os.cpu_count(),
+                 "kind": "port", "sample": f"{sample}, oracle/fa_oracle.c on {nt} OpenMP threads, {reps} reps, "
+                 f"{dt * 1e3:.0f} ms/rep"}, ref)
     # c5: the whole config
     qh, kh, vh = bits(q), bits(kc), bits(vc)
-    dt, reps = _timed(lambda: orc.kvcache_forward(qh, kh, vh, dtype=orc.BF16, cache_seqlens=L.numpy(),
-                                                  cache_batch_idx=bidx.cpu().numpy(), block_table=bt.cpu().numpy(),
-                                                  causal=True, window=(4096, 0), alibi=alibi.cpu().numpy(),
-                                                  nthreads=nt))
-    return {"value": round(c["attn_bytes"] / dt / 1e12, 6), "unit": "TB/s", "cores": nt,
-            "host_cores": os.cpu_count(), "kind": "port",
-            "sample": f"config 5, all {c['B']} sequences, oracle/fa_oracle.c on {nt} OpenMP threads, {reps} reps, "
-                      f"{dt * 1e3:.1f} ms/rep"}
+    res = {}
+
+    def run():
+        res["r"] = orc.kvcache_forward(qh, kh, vh, dtype=orc.BF16, cache_seqlens=L.numpy(),
+                                       cache_batch_idx=bidx.cpu().numpy(), block_table=bt.cpu().numpy(), causal=True,
+                                       window=(4096, 0), alibi=alibi.cpu().numpy(), nthreads=nt)
+    dt, reps = _timed(run)
+    ro, rl, _, _ = res["r"]
+    ref = {"out": ro, "lse": rl, "k": None, "v": None, "sel_q": lambda t: t, "sel_kv": None,
+           "sample": f"config 5, all {c['B']} sequences (no append)"}
+    return ({"value": round(c["attn_bytes"] / dt / 1e12, 6), "unit": "TB/s", "cores": nt,
+             "host_cores": os.cpu_count(), "kind": "port",
+             "sample": f"config 5, all {c['B']} sequences, oracle/fa_oracle.c on {nt} OpenMP threads, {reps} reps, "
+                       f"{dt * 1e3:.1f} ms/rep"}, ref)
+
+
+def parity(c, ref, torch):
+    """The GPU's result on the benchmarked inputs against the oracle's on the
+    cpu_baseline sample: one more call on the first cache copy (the one the
+    oracle ran on), then out max-abs against the bf16 bar of 1e-2 (plus half
+    an ulp of the reference value: the oracle's output is itself rounded to
+    bf16), LSE relative error against 1e-4 (with a 1e-5 absolute floor for
+    |LSE| < 0.1), and the cache after the append bit for bit."""
+    import numpy as np
+    from fa_mi355x import capi
+    from oracle import fa_oracle as orc
+    q, kn, vn, caches, bt, bidx, cos, sin, alibi, out, lse = c["keep"][:11]
+    p = c["params"][0]
+    p.stage_events = None
+    st = capi.lib().fa_mha_fwd_kvcache(ctypes.byref(p), torch.cuda.current_stream().cuda_stream)
+    if st != 0:
+        raise RuntimeError(capi.last_error())
+    torch.cuda.synchronize()
+    bits = lambda t: t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+    got = ref["sel_q"](out).float().cpu().numpy()
+    want = orc.from_bits(ref["out"], orc.BF16).reshape(got.shape)
+    err = np.abs(got - want)
+    out_ok = bool((err <= 1e-2 + np.abs(want) * 2.0 ** -8).all()) and not np.isnan(got).any()
+    gl = ref["sel_q"](lse).cpu().numpy().astype(np.float64)
+    rl = np.asarray(ref["lse"], dtype=np.float64).reshape(gl.shape)
+    fin = np.isfinite(rl)
+    dl = np.abs(gl[fin] - rl[fin])
+    lse_ok = bool(np.array_equal(np.isinf(gl), np.isinf(rl)) and (dl <= 1e-4 * np.abs(rl[fin]) + 1e-5).all())
+    r = {"out_max_abs": float(err.max()), "out_tol": 1e-2, "lse_max_rel": float((dl / np.abs(rl[fin])).max()),
+         "lse_tol_rel": 1e-4, "sample": ref["sample"]}
+    if ref["k"] is not None:
+        kc, vc = caches[0]
+        r["cache_bit_exact"] = bool(np.array_equal(bits(ref["sel_kv"](kc)), ref["k"]) and
+                                    np.array_equal(bits(ref["sel_kv"](vc)), ref["v"]))
+    else:
+        r["cache_bit_exact"] = None
+    r["ok"] = out_ok and lse_ok and r["cache_bit_exact"] is not False
+    return r
 
 
 def ceilings(torch, hip):
@@ -411,22 +480,6 @@ def ceilings(torch, hip):
     res["gemm_bf16_tflops"] = round(2 * n ** 3 / t / 1e12, 1)
     res["note"] = "4 GiB bf16 copy (2 x 4 GiB moved), torch.sum of 4 GiB bf16, 8192^3 bf16 torch.matmul"
     torch.cuda.empty_cache()
-    # LDS read rates (bytes per shader clock per CU) of the kernels' access
-    # patterns, from the probe library build.py makes (csrc/probes/fa_lds_probe.hip)
-    probe = os.path.join(REPO, "flash-attention-npu_amd", "fa_mi355x", "lib", "libfa_lds_probe.so")
-    if os.path.exists(probe):
-        L = ctypes.CDLL(probe, mode=os.RTLD_LOCAL)
-        L.fa_lds_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
-        names = ["b128_row", "b64_tr16", "b64", "2xb64_plane_split", "2xb64_naive", "read2st64_b64", "read2_b64"]
-        lds = {}
-        for pat, nm in enumerate(names):
-            for waves in (8, 16):
-                v = ctypes.c_double()
-                st = L.fa_lds_probe(pat, waves, ctypes.byref(v))
-                if st != 0:
-                    raise RuntimeError(f"fa_lds_probe({pat}, {waves}) failed: {st}")
-                lds[f"{nm}_w{waves}"] = round(v.value, 1)
-        res["lds_bytes_per_clk_per_cu"] = lds
     return res
 
 
@@ -478,19 +531,29 @@ def bench_bwd(torch, hip, steps, warmup):
             "workload": f"backward, dense causal B{B} S{S} H{H}/{Hk} D{D} bf16 (dsum + dK/dV + dQ kernels)"}
 
 
-TRAFFIC_PROFILE = "profiles/fa_attention_kernels_hbm_traffic.txt"
+TRAFFIC_PROFILES = ("profiles/fa_attention_kernels_hbm_traffic.txt", "profiles/fa_decode_kernel_fp8_hbm_traffic.txt")
+
+
+def traffic_source(cfg):
+    """The profile summary that holds `cfg`'s measured traffic, or None."""
+    import re
+    for rel in TRAFFIC_PROFILES:
+        path = os.path.join(REPO, rel)
+        if os.path.exists(path) and re.search(r"^traffic_bytes_per_launch\[%s\]\s*=" % cfg, open(path).read(), re.M):
+            return rel
+    return None
 
 
 def measured_traffic(cfg):
     """HBM bytes per launch of the attention kernel on `cfg`, as measured by the two
-    rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) summarised in TRAFFIC_PROFILE
+    rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) summarised in TRAFFIC_PROFILES
     (scaled by the plain-copy calibration recorded there); None if absent."""
     import re
-    path = os.path.join(REPO, TRAFFIC_PROFILE)
-    if not os.path.exists(path):
+    rel = traffic_source(cfg)
+    if rel is None:
         return None
-    m = re.search(r"^traffic_bytes_per_launch\[%s\]\s*=\s*(\d+)" % cfg, open(path).read(), re.M)
-    return int(m.group(1)) if m else None
+    m = re.search(r"^traffic_bytes_per_launch\[%s\]\s*=\s*(\d+)" % cfg, open(os.path.join(REPO, rel)).read(), re.M)
+    return int(m.group(1))
 
 
 PHASES_LIB = os.path.join(REPO, "flash-attention-npu_amd", "fa_mi355x", "lib", "libfa_mi355x_phases.so")
@@ -510,6 +573,8 @@ def decode_phases(names, torch, hip, reps):
     plus the median exit per XCD and per segment count."""
     import numpy as np
     from fa_mi355x import capi
+    if not os.path.exists(PHASES_LIB):
+        raise SystemExit(f"{PHASES_LIB} is not built: run python flash-attention-npu_amd/build.py --phases first")
     L = ctypes.CDLL(PHASES_LIB, mode=os.RTLD_LOCAL)
     L.fa_mha_fwd_kvcache.argtypes = [ctypes.POINTER(capi.FwdParams), ctypes.c_void_p]
     L.fa_decode_phase_stamps.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int)]
@@ -644,7 +709,8 @@ def main():
             r["attn_frac_hbm"] = r["attn_tbps"] * 1e3 / HBM_PEAK_GBS
             r["roofline"] = {"bound": "hbm", "achieved": round(r["attn_tbps"] * 1e3, 1), "peak": HBM_PEAK_GBS,
                              "unit": "GB/s", "frac": round(r["attn_frac_hbm"], 4),
-                             "traffic": measured_traffic(name), "kernel": "fa_decode_kernel",
+                             "traffic": measured_traffic(name), "traffic_source": traffic_source(name),
+                             "kernel": "fa_decode_kernel",
                              "kernel_us": round(t["attn_us"], 2), "algorithmic_bytes": c["attn_bytes"]}
         else:
             r["flops_per_call"] = c["flops"]
@@ -656,7 +722,8 @@ def main():
                              "kernel": "fa_prefill_kernel", "kernel_us": round(t["attn_us"], 2),
                              "algorithmic_flops": c["flops"]}
         if not args.no_cpu and name in ("c2", "c3", "c4", "c5"):
-            r["cpu_baseline"] = cpu_baseline(c, torch)
+            r["cpu_baseline"], ref = cpu_baseline(c, torch)
+            r["parity"] = parity(c, ref, torch)
         results[name] = r
         print(f"# {name}: {json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})}",
               file=sys.stderr, flush=True)
@@ -672,6 +739,7 @@ def main():
         del src, dst
     c2 = results["c2"]
     traffic = measured_traffic("c2")
+    traffic_src = traffic_source("c2")
     cpu = c2.get("cpu_baseline")
     if args.ceilings:
         results["ceilings"] = ceilings(torch, hip)
@@ -696,8 +764,9 @@ def main():
                      "unit": "GB/s", "frac": round(c2["attn_frac_hbm"], 4), "traffic": traffic,
                      "kernel": "fa_decode_kernel", "kernel_us": round(c2["attn_us"], 2),
                      "algorithmic_bytes": c2["attn_bytes"],
-                     "traffic_source": TRAFFIC_PROFILE if traffic is not None else None},
+                     "traffic_source": traffic_src},
         "cpu_baseline": cpu,
+        "parity": c2.get("parity"),
         "configs": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in results.items()},
         "host_cores": os.cpu_count(),

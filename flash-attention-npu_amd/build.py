@@ -2,12 +2,13 @@
 
   fa_mi355x/lib/libfa_mi355x.so        HIP kernels for gfx950 + the C ABI (include/fa_mi355x.h)
   fa_mi355x/lib/libfa_mi355x_torch.so  torch.ops.fa_mi355x operators over that C ABI
-  fa_mi355x/lib/libfa_mi355x_phases.so the same C ABI with per-wave real-time
-                                       stamps in the decode kernel (FA_DECODE_PHASES),
-                                       read by bench.py --phases; never loaded otherwise
+  fa_mi355x/lib/libfa_mi355x_phases.so (only with --phases) the same C ABI with
+                                       per-wave real-time stamps in the decode kernel
+                                       (FA_DECODE_PHASES), read by bench.py --phases;
+                                       never loaded otherwise
 
-Usage: python build.py [--jobs N]. hipcc cross-compiles for gfx950, so this
-runs on a machine without a GPU.
+Usage: python build.py [--jobs N] [--phases]. hipcc cross-compiles for gfx950,
+so this runs on a machine without a GPU.
 """
 import argparse
 import os
@@ -80,7 +81,7 @@ def _torch_flags():
     return cflags, ldflags
 
 
-def build(jobs=8, verbose=True):
+def build(jobs=8, verbose=True, phases=False):
     os.makedirs(LIBDIR, exist_ok=True)
     os.makedirs(OBJDIR, exist_ok=True)
     cflags, ldflags = _torch_flags()
@@ -88,27 +89,22 @@ def build(jobs=8, verbose=True):
     torch_cmd = ["g++"] + cflags + ["-c", os.path.join(CSRC, "torch_ext", "fa_torch_ops.cpp"), "-o", torch_obj]
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         futs = [ex.submit(_compile_hip, s) for s in HIP_SOURCES]
-        pfut = ex.submit(_compile_hip, "fa_decode.hip", ("FA_DECODE_PHASES",), ".phases")
-        lfut = ex.submit(_compile_hip, os.path.join("probes", "fa_lds_probe.hip"))
+        pfut = ex.submit(_compile_hip, "fa_decode.hip", ("FA_DECODE_PHASES",), ".phases") if phases else None
         tfut = ex.submit(_run, torch_cmd)
         objs = [f.result() for f in futs]
-        pobj = pfut.result()
-        lobj = lfut.result()
+        pobj = pfut.result() if phases else None
         tfut.result()
     core = os.path.join(LIBDIR, "libfa_mi355x.so")
     tmp = core + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", tmp] + objs)
     os.replace(tmp, core)
-    phases = os.path.join(LIBDIR, "libfa_mi355x_phases.so")
-    pobjs = [pobj if os.path.basename(o) == "fa_decode.hip.o" else o for o in objs]
-    # -Bsymbolic: the instrumented library binds its own kernels even beside the product library
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-Wl,-Bsymbolic", "-o", phases + ".tmp"]
-         + pobjs)
-    os.replace(phases + ".tmp", phases)
-    # the LDS read-rate probe behind the kernels' LDS layouts (bench.py --ceilings)
-    probe = os.path.join(LIBDIR, "libfa_lds_probe.so")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", probe + ".tmp", lobj])
-    os.replace(probe + ".tmp", probe)
+    if phases:
+        plib = os.path.join(LIBDIR, "libfa_mi355x_phases.so")
+        pobjs = [pobj if os.path.basename(o) == "fa_decode.hip.o" else o for o in objs]
+        # -Bsymbolic: the instrumented library binds its own kernels even beside the product library
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-Wl,-Bsymbolic", "-o",
+              plib + ".tmp"] + pobjs)
+        os.replace(plib + ".tmp", plib)
     tlib = os.path.join(LIBDIR, "libfa_mi355x_torch.so")
     tmp = tlib + ".tmp"
     _run(["g++", "-shared", "-o", tmp, torch_obj, "-L", LIBDIR, "-lfa_mi355x", "-Wl,-rpath,$ORIGIN"] + ldflags)
@@ -127,8 +123,10 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=8)
     ap.add_argument("--clean", action="store_true")
+    ap.add_argument("--phases", action="store_true",
+                    help="also build libfa_mi355x_phases.so (decode kernel with per-wave stamps, bench.py --phases)")
     args = ap.parse_args()
     if args.clean:
         clean()
-    build(args.jobs)
+    build(args.jobs, phases=args.phases)
     sys.exit(0)

@@ -337,10 +337,11 @@ fa_status_t run_forward_ws(const fa_fwd_params* p, int kind, void* stream_v, voi
     // tokens (the first row sees its own diagonal key), or no left window and
     // no attention chunk (every tile from key 0 is visited); ragged q (a
     // sequence may have no query rows, hence no tiles) takes the separate
-    // append, as does a batch run in chunks.
+    // append, as does a batch run in chunks, and a call with no query rows
+    // (it launches no attention kernel at all).
     const bool local_left = p->window_size_left >= 0 || p->attention_chunk > 0;
     const bool fused_append = kind == FA_KIND_KVCACHE && p->k_new && pl.decode && !pl.rotary && !p->cu_seqlens_k_new &&
-                              !p->cu_seqlens_q && !chunked && !p->no_pack_gqa &&
+                              !p->cu_seqlens_q && !chunked && !p->no_pack_gqa && p->seqlen_q > 0 &&
                               (p->seqlen_new <= p->seqlen_q || !local_left);
     if (kind == FA_KIND_KVCACHE && p->k_new && !fused_append) {
         fa::KvPrepArgs k{};

@@ -713,7 +713,7 @@ TORCH_LIBRARY(fa_mi355x, m) {
     m.def(
         "fwd(Tensor q, Tensor k, Tensor v, Tensor? alibi_slopes, float p_dropout, float softmax_scale, bool is_causal, "
         "int window_size_left, int window_size_right, float softcap, int attention_chunk=0, Tensor? q_descale=None, "
-        "Tensor? k_descale=None, Tensor? v_descale=None, int num_splits=0, Tensor? workspace=None, "
+        "Tensor? k_descale=None, Tensor? v_descale=None, int num_splits=0, Tensor(a!)? workspace=None, "
         "bool? pack_gqa=None) -> (Tensor, Tensor)");
     m.def(
         "fwd_kvcache_v3(Tensor q, Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor? k, Tensor? v, Tensor? seqlens_k, "
@@ -721,7 +721,7 @@ TORCH_LIBRARY(fa_mi355x, m) {
         "Tensor? alibi_slopes, Tensor? cu_seqlens_q, Tensor? cu_seqlens_k_new, int max_seqlen_q, "
         "Tensor? rotary_seqlens, float softmax_scale, bool is_causal, int window_size_left, int window_size_right, "
         "int attention_chunk, float softcap, bool is_rotary_interleaved, int num_splits, Tensor? q_descale=None, "
-        "Tensor? k_descale=None, Tensor? v_descale=None, Tensor? workspace=None, Tensor? qv=None, "
+        "Tensor? k_descale=None, Tensor? v_descale=None, Tensor(c!)? workspace=None, Tensor? qv=None, "
         "bool? pack_gqa=None) -> (Tensor, Tensor)");
     m.def(
         "varlen_fwd(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor? cu_seqlens_k, Tensor? seqused_k, "
@@ -729,7 +729,7 @@ TORCH_LIBRARY(fa_mi355x, m) {
         "Tensor? alibi_slopes, int max_seqlen_q, int max_seqlen_k, float p_dropout, float softmax_scale, "
         "bool is_causal, int window_size_left, int window_size_right, float softcap, int attention_chunk=0, "
         "Tensor? q_descale=None, Tensor? k_descale=None, Tensor? v_descale=None, int num_splits=0, "
-        "Tensor? workspace=None, bool? pack_gqa=None) -> (Tensor, Tensor)");
+        "Tensor(a!)? workspace=None, bool? pack_gqa=None) -> (Tensor, Tensor)");
     m.def("fwd_combine(Tensor out_partial, Tensor lse_partial, ScalarType? out_dtype) -> (Tensor, Tensor)");
     m.def("fwd_combine_out(Tensor out_partial, Tensor lse_partial, Tensor(a!) out) -> Tensor");
     m.def(

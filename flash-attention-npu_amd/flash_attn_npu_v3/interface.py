@@ -74,6 +74,10 @@ def _describe(batch, max_seqlen_q, max_seqlen_k, nheads, nheads_k, headdim, head
     wr = -1 if window_size[1] < 0 else int(window_size[1])
     if causal:
         wr = 0
+    if dtype in (torch.float16, torch.bfloat16):
+        # the head dims the kernels run at: 16-bit rows are zero-padded to a
+        # multiple of 8 (_needs_pad), so a call and its padded form share a plan
+        headdim, headdim_v = -(-int(headdim) // 8) * 8, -(-int(headdim_v) // 8) * 8
     return dict(batch=int(batch), max_seqlen_q=int(max_seqlen_q), max_seqlen_k=int(max_seqlen_k), nheads=int(nheads),
                 nheads_k=int(nheads_k), headdim=int(headdim), headdim_v=int(headdim_v), dtype=_dtype_code(dtype),
                 causal=int(bool(causal)), window_left=wl, window_right=wr, attention_chunk=int(attention_chunk),
@@ -82,13 +86,51 @@ def _describe(batch, max_seqlen_q, max_seqlen_k, nheads, nheads_k, headdim, head
 
 
 def _plan_workspace(d):
-    """Largest workspace any call of this description needs (the kvcache call
-    with rotary included), from the library's own planner."""
+    """Largest workspace any call of this description needs, from the
+    library's own planner: every query length up to max_seqlen_q, packed and
+    unpacked GQA, and the kvcache call with rotary included.
+
+    Within each kernel regime the planner's need grows with the query length
+    (decode: <= 16 packed rows per kv head, its rotated-q copy grows; prefill
+    split over the key range while batch x kv heads x row tiles leave CUs
+    idle, its partial rows grow; prefill unsplit: no partials), and the
+    regimes follow one another in that order as the query length grows. So
+    the largest need is at the right end of a regime: the last decode length,
+    the last split length (found by bisection) or max_seqlen_q."""
+    maxq = max(d["max_seqlen_q"], 1)
+    g = d["nheads"] // max(d["nheads_k"], 1)
+    need = None
+    for no_pack in (0, 1):
+        ge = 1 if no_pack else max(g, 1)
+        need_at = lambda sq: _workspace_at(d, sq, no_pack)  # noqa: E731
+        base = need_at(maxq)
+        lengths = {1, maxq, min(maxq, max(1, 16 // ge))}
+        # the last length whose plan has partial rows (decode or split prefill);
+        # `bare` is a plan without any: unsplit prefill (17 unpacked rows)
+        bare = _workspace_at(dict(d, num_splits=1), 17, 1)
+        if need_at(1) > bare:
+            lo, hi = 1, maxq
+            while lo < hi:
+                mid = (lo + hi + 1) // 2
+                if need_at(mid) > bare:
+                    lo = mid
+                else:
+                    hi = mid - 1
+            lengths.add(lo)
+        for sq in lengths:
+            n = base if sq == maxq else need_at(sq)
+            need = n if need is None else max(need, n)
+    return need
+
+
+def _workspace_at(d, Sq, no_pack):
+    """The planner's workspace for the calls of description `d` at query
+    length Sq (the largest over the call kinds the description allows)."""
     from fa_mi355x import capi
-    B, Sq, Sk, H, Hk, D = d["batch"], max(d["max_seqlen_q"], 1), max(d["max_seqlen_k"], 1), d["nheads"], \
-        d["nheads_k"], d["headdim"]
+    B, Sk, H, Hk, D = d["batch"], max(d["max_seqlen_k"], 1), d["nheads"], d["nheads_k"], \
+        -(-d["headdim"] // 8) * 8
     dummy = 1 << 20  # aligned stand-in addresses: the planner never dereferences them
-    common = dict(dtype=d["dtype"], batch=B, seqlen_q=Sq, nheads=H, nheads_k=Hk, headdim=D, headdim_v=d["headdim_v"],
+    common = dict(dtype=d["dtype"], batch=B, seqlen_q=Sq, nheads=H, nheads_k=Hk, headdim=D, headdim_v=D,
                   q=dummy, q_batch_stride=Sq * H * D, q_row_stride=H * D, q_head_stride=D,
                   k=dummy, k_batch_stride=Sk * Hk * D, k_row_stride=Hk * D, k_head_stride=D,
                   v=dummy, v_batch_stride=Sk * Hk * D, v_row_stride=Hk * D, v_head_stride=D,
@@ -96,7 +138,7 @@ def _plan_workspace(d):
                   softmax_lse=dummy, softmax_scale=1.0, is_causal=d["causal"],
                   window_size_left=d["window_left"], window_size_right=d["window_right"],
                   attention_chunk=d["attention_chunk"], softcap=1.0 if d["softcap"] else 0.0,
-                  num_splits=d["num_splits"])
+                  num_splits=d["num_splits"], no_pack_gqa=no_pack)
     if d["varlen_q"]:
         common.update(cu_seqlens_q=dummy, total_q=B * Sq)
     cands = []
@@ -172,6 +214,31 @@ def _pack(pack_gqa):
     return None if pack_gqa is None else bool(pack_gqa)
 
 
+def _needs_pad(x):
+    """16-bit inputs whose head dim is not a multiple of 8: the kernels load
+    16-byte chunks of a head row, so such rows are zero-padded to the next
+    multiple of 8 (zeros add nothing to q.k and give zero output columns,
+    which are sliced off). The reference v3 accepts any head dim <= 256
+    (csrc/arch22/flash_attn_npu_v3/flash_api.cpp:201-218); FP8 keeps its own
+    multiple-of-16 rule."""
+    return x is not None and x.shape[-1] % 8 != 0 and x.dtype in (torch.float16, torch.bfloat16)
+
+
+def _pad_last(x, width):
+    return x if x is None or x.shape[-1] == width else torch.nn.functional.pad(x, [0, width - x.shape[-1]])
+
+
+def _padded_head(attn, q, k, v, return_lse):
+    """attn(q, k, v) on rows zero-padded to a multiple of 8 (differentiable:
+    the gradient of the padding is the slice), output sliced back."""
+    dv = v.shape[-1]
+    w = -(-max(q.shape[-1], dv) // 8) * 8
+    res = attn(_pad_last(q, w), _pad_last(k, w), _pad_last(v, w))
+    if return_lse:
+        return res[0][..., :dv], res[1]
+    return res[..., :dv]
+
+
 def _qv_by_concat(attn, q, k, v, qv, return_lse):
     """FlashAttention-3's qv for the prefill kernels: scores = q.k + qv.v is
     one attention over the head dims of q and qv concatenated, against k and
@@ -183,7 +250,7 @@ def _qv_by_concat(attn, q, k, v, qv, return_lse):
     q2 = torch.cat([q, qv], dim=-1)
     k2 = torch.cat([k, v], dim=-1)
     v2 = torch.cat([v, torch.zeros_like(k)], dim=-1)
-    res = attn(q2, k2, v2)
+    res = _padded_head(attn, q2, k2, v2, return_lse) if _needs_pad(q2) else attn(q2, k2, v2)
     if return_lse:
         return res[0][..., :dv], res[1]
     return res[..., :dv]
@@ -286,6 +353,13 @@ def flash_attn_func(q, k, v, softmax_scale=None, causal=False, qv=None, q_descal
             q2, k2, v2, softmax_scale, causal, None, q_descale, k_descale, v_descale, window_size, attention_chunk,
             softcap, num_splits, pack_gqa, deterministic, sm_margin, return_attn_probs, scheduler_metadata),
             q, k, v, qv, return_attn_probs)
+    if _needs_pad(q):
+        if softmax_scale is None:
+            softmax_scale = q.shape[-1] ** (-0.5)
+        return _padded_head(lambda q2, k2, v2: FlashAttnFunc.apply(
+            q2, k2, v2, softmax_scale, causal, None, q_descale, k_descale, v_descale, window_size, attention_chunk,
+            softcap, num_splits, pack_gqa, deterministic, sm_margin, return_attn_probs,
+            scheduler_metadata), q, k, v, return_attn_probs)
     return FlashAttnFunc.apply(q, k, v, softmax_scale, causal, qv, q_descale, k_descale, v_descale, window_size,
                                attention_chunk, softcap, num_splits, pack_gqa, deterministic, sm_margin,
                                return_attn_probs, scheduler_metadata)
@@ -307,6 +381,14 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
             softmax_scale, causal, None, q_descale, k_descale, v_descale, window_size, attention_chunk, softcap,
             num_splits, pack_gqa, deterministic, sm_margin, return_attn_probs, scheduler_metadata),
             q, k, v, qv, return_attn_probs)
+    if _needs_pad(q):
+        if softmax_scale is None:
+            softmax_scale = q.shape[-1] ** (-0.5)
+        return _padded_head(lambda q2, k2, v2: FlashAttnVarlenFunc.apply(
+            q2, k2, v2, cu_seqlens_q, cu_seqlens_k, seqused_q, seqused_k, max_seqlen_q, max_seqlen_k,
+            softmax_scale, causal, None, q_descale, k_descale, v_descale, window_size, attention_chunk, softcap,
+            num_splits, pack_gqa, deterministic, sm_margin, return_attn_probs,
+            scheduler_metadata), q, k, v, return_attn_probs)
     return FlashAttnVarlenFunc.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_q, seqused_k, max_seqlen_q,
                                      max_seqlen_k, softmax_scale, causal, qv, q_descale, k_descale, v_descale,
                                      window_size, attention_chunk, softcap, num_splits, pack_gqa, deterministic,
@@ -369,6 +451,16 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None, rotary
     ws, md_splits = _metadata_for(scheduler_metadata, call, q.device)
     if md_splits is not None:
         num_splits = md_splits
+    pad_d = _needs_pad(q)
+    if pad_d:
+        # head dims not a multiple of 8 (_needs_pad): the call runs on
+        # zero-padded copies of q, k / v, qv and the caches; the caches'
+        # real columns are copied back after an append, and out is sliced
+        d_og, dv_og = q.shape[-1], v_cache.shape[-1]
+        w = -(-max(d_og, dv_og) // 8) * 8
+        kc_user, vc_user = k_cache, v_cache
+        k_cache, v_cache = _pad_last(k_cache, w), _pad_last(v_cache, w)
+        q, k, v, qv = (_pad_last(x, w) for x in (q, k, v, qv))
     q, k, v = [maybe_contiguous(x) for x in (q, k, v)]
     if cu_seqlens_q is not None and max_seqlen_q is None:
         raise RuntimeError("max_seqlen_q is required with cu_seqlens_q")
@@ -399,6 +491,11 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None, rotary
                                               int(window_size[1]), int(attention_chunk), float(softcap),
                                               bool(rotary_interleaved), int(num_splits), q_descale, k_descale,
                                               v_descale, ws, maybe_contiguous(qv), _pack(pack_gqa))
+    if pad_d:
+        out = out[..., :dv_og]
+        if k is not None:
+            kc_user.copy_(k_cache[..., :d_og])
+            vc_user.copy_(v_cache[..., :dv_og])
     if return_softmax_lse:
         oa, la = _empty_accum(out)
         return out, softmax_lse, oa, la

@@ -118,6 +118,26 @@ uint16_t orc_f32_to_f16(float f) {
 static inline float to_f32(int dtype, uint16_t h) {
     return dtype == ORC_BF16 ? orc_bf16_to_f32(h) : orc_f16_to_f32(h);
 }
+
+/* The same conversion through a table for fp16 (every one of the 65536 values
+ * decoded once by orc_f16_to_f32), for the inner loops of the attention. The
+ * table is filled by orc_attention before its parallel region. */
+static float g_f16_lut[65536];
+static int g_f16_lut_ready = 0;
+static void fill_f16_lut(void) {
+    if (g_f16_lut_ready) return;
+    for (uint32_t h = 0; h < 65536u; h++) g_f16_lut[h] = orc_f16_to_f32((uint16_t)h);
+    g_f16_lut_ready = 1;
+}
+static inline float cvt(int dtype, uint16_t h) {
+    if (dtype == ORC_BF16) {
+        uint32_t u = (uint32_t)h << 16;
+        float f;
+        memcpy(&f, &u, 4);
+        return f;
+    }
+    return g_f16_lut[h];
+}
 static inline uint16_t from_f32(int dtype, float f) {
     return dtype == ORC_BF16 ? orc_f32_to_bf16(f) : orc_f32_to_f16(f);
 }
@@ -150,6 +170,7 @@ static inline int key_visible(int i, int j, int sq, int sk, int wl, int wr, int 
 /* ---- the blockwise golden (ref_flash_attention) ----------------------------- */
 
 #define ORC_STACK 512
+#define ORC_ROWS 16 /* query rows per unit of parallel work */
 
 static const uint16_t* key_row(const orc_fwd_params* p, int b, int j, int hk, int is_v) {
     const uint16_t* base = is_v ? p->v : p->k;
@@ -197,17 +218,60 @@ static void attention_row(const orc_fwd_params* p, int b, int i, int h, int sq, 
         int n = sk - j0 < ORC_STACK ? sk - j0 : ORC_STACK;
         int nvis = 0;
         float lm = -INFINITY;
+        int vis[ORC_STACK];
         for (int t = 0; t < n; t++) {
-            int j = j0 + t;
-            if (!key_visible(i, j, sq, sk, p->wl, p->wr, p->chunk)) { s[t] = -INFINITY; continue; }
-            const uint16_t* kr = key_row(p, b, j, hk, 0);
-            float acc = 0.f;
-            for (int d = 0; d < D; d++) acc += qf[d] * to_f32(dt, kr[d]);
-            if (p->qv) {
-                const uint16_t* vr = key_row(p, b, j, hk, 1);
-                for (int d = 0; d < Dv; d++) acc += qvf[d] * to_f32(dt, vr[d]);
+            if (!key_visible(i, j0 + t, sq, sk, p->wl, p->wr, p->chunk)) s[t] = -INFINITY;
+            else vis[nvis++] = t;
+        }
+        /* q . k of the visible keys, four keys at a time: every key keeps its
+         * own fp32 accumulator summed in head-dim order (then qv . v in the
+         * same accumulator), so each score is what a one-key loop gives */
+        float acc[ORC_STACK];
+        int u = 0;
+        for (; u + 4 <= nvis; u += 4) {
+            const uint16_t* k0 = key_row(p, b, j0 + vis[u], hk, 0);
+            const uint16_t* k1 = key_row(p, b, j0 + vis[u + 1], hk, 0);
+            const uint16_t* k2 = key_row(p, b, j0 + vis[u + 2], hk, 0);
+            const uint16_t* k3 = key_row(p, b, j0 + vis[u + 3], hk, 0);
+            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+            for (int d = 0; d < D; d++) {
+                const float qd = qf[d];
+                a0 += qd * cvt(dt, k0[d]);
+                a1 += qd * cvt(dt, k1[d]);
+                a2 += qd * cvt(dt, k2[d]);
+                a3 += qd * cvt(dt, k3[d]);
             }
-            float x = acc * p->scale;
+            if (p->qv) {
+                const uint16_t* v0 = key_row(p, b, j0 + vis[u], hk, 1);
+                const uint16_t* v1 = key_row(p, b, j0 + vis[u + 1], hk, 1);
+                const uint16_t* v2 = key_row(p, b, j0 + vis[u + 2], hk, 1);
+                const uint16_t* v3 = key_row(p, b, j0 + vis[u + 3], hk, 1);
+                for (int d = 0; d < Dv; d++) {
+                    const float qd = qvf[d];
+                    a0 += qd * cvt(dt, v0[d]);
+                    a1 += qd * cvt(dt, v1[d]);
+                    a2 += qd * cvt(dt, v2[d]);
+                    a3 += qd * cvt(dt, v3[d]);
+                }
+            }
+            acc[u] = a0;
+            acc[u + 1] = a1;
+            acc[u + 2] = a2;
+            acc[u + 3] = a3;
+        }
+        for (; u < nvis; u++) {
+            const uint16_t* kr = key_row(p, b, j0 + vis[u], hk, 0);
+            float a = 0.f;
+            for (int d = 0; d < D; d++) a += qf[d] * cvt(dt, kr[d]);
+            if (p->qv) {
+                const uint16_t* vr = key_row(p, b, j0 + vis[u], hk, 1);
+                for (int d = 0; d < Dv; d++) a += qvf[d] * cvt(dt, vr[d]);
+            }
+            acc[u] = a;
+        }
+        for (u = 0; u < nvis; u++) {
+            const int t = vis[u], j = j0 + t;
+            float x = acc[u] * p->scale;
             if (p->softcap > 0.f) x = p->softcap * tanhf(x / p->softcap);
             if (p->alibi) {
                 long dist = (long)i + sk - sq - j;
@@ -216,7 +280,6 @@ static void attention_row(const orc_fwd_params* p, int b, int i, int h, int sq, 
             }
             s[t] = x;
             if (x > lm) lm = x;
-            nvis++;
         }
         /* A stack with no visible key adds exactly zero once a later stack
          * rescales it (exp(-1e4 - m) underflows in fp32 in the golden); skipping
@@ -238,7 +301,8 @@ static void attention_row(const orc_fwd_params* p, int b, int i, int h, int sq, 
         for (int t = 0; t < n; t++) {
             if (pr[t] == 0.f) continue;
             const uint16_t* vr = key_row(p, b, j0 + t, hk, 1);
-            for (int d = 0; d < Dv; d++) lo[d] += pr[t] * to_f32(dt, vr[d]);
+            const float pt = pr[t];
+            for (int d = 0; d < Dv; d++) lo[d] += pt * cvt(dt, vr[d]);
         }
         if (!started) {
             gl = row_sum;
@@ -262,24 +326,32 @@ static void attention_row(const orc_fwd_params* p, int b, int i, int h, int sq, 
 int orc_attention(const orc_fwd_params* p) {
     if (p->D > 1024 || p->Dv > 1024 || p->H % p->Hk) return -1;
     const int B = p->B, H = p->H;
-    int64_t total_rows = 0;
+    int nthreads = p->nthreads > 0 ? p->nthreads : 1;
+    if (p->dtype != ORC_BF16) fill_f16_lut();
+    /* rows are independent: the work is cut into chunks of ORC_ROWS query rows
+     * of one (batch, head), so a few long sequences still use every thread */
+    int max_sq = 0;
     for (int b = 0; b < B; b++) {
         int sq = p->cu_seqlens_q ? p->cu_seqlens_q[b + 1] - p->cu_seqlens_q[b] : p->Sq;
-        total_rows += (int64_t)sq * H;
+        if (sq > max_sq) max_sq = sq;
     }
-    (void)total_rows;
-    int nthreads = p->nthreads > 0 ? p->nthreads : 1;
+    const int64_t nchunk = (max_sq + ORC_ROWS - 1) / ORC_ROWS;
+    const int64_t nwork = (int64_t)B * H * nchunk;
 #pragma omp parallel num_threads(nthreads)
     {
         float* s = (float*)malloc(sizeof(float) * ORC_STACK);
         float* pr = (float*)malloc(sizeof(float) * ORC_STACK);
-#pragma omp for schedule(dynamic, 1) collapse(2)
-        for (int b = 0; b < B; b++) {
-            for (int h = 0; h < H; h++) {
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t w = 0; w < nwork; w++) {
+            {
+                const int b = (int)(w / ((int64_t)H * nchunk));
+                const int h = (int)((w / nchunk) % H);
+                const int i0 = (int)(w % nchunk) * ORC_ROWS;
                 int sq = p->cu_seqlens_q ? p->cu_seqlens_q[b + 1] - p->cu_seqlens_q[b] : p->Sq;
                 int sk = p->seqlens_k ? p->seqlens_k[b]
                        : (p->cu_seqlens_k ? p->cu_seqlens_k[b + 1] - p->cu_seqlens_k[b] : p->Sk);
-                for (int i = 0; i < sq; i++) {
+                const int i1 = i0 + ORC_ROWS < sq ? i0 + ORC_ROWS : sq;
+                for (int i = i0; i < i1; i++) {
                     int64_t orow = p->cu_seqlens_q ? ((int64_t)p->cu_seqlens_q[b] + i) * p->o_si
                                                    : (int64_t)b * p->o_sb + (int64_t)i * p->o_si;
                     uint16_t* o = p->out + orow + (int64_t)h * p->o_sh;

@@ -2,21 +2,27 @@
 public flash_attn_func / flash_attn_varlen_func (v2 and v3) against the
 float64 backward oracle (oracle/fa_bwd_oracle.py), fed with the inputs and the
 forward's own LSE exactly as the reference tests feed their golden
-(tests/test_flash_attn_npu_v2_bwd.py:76-138 in the reference).
+(tests/test_flash_attn_npu_v2_bwd.py:76-138 in the reference). That forward
+(out and LSE) is itself checked against the forward oracle first.
 
 Bar, the reference's: |got - ref| <= 1e-2 + 1e-2 * |ref| elementwise
 (RTOL_GOLDEN = ATOL_GOLDEN = 1e-2, test_flash_attn_npu_v2_bwd.py:27-28), on
 inputs uniform in [-1, 1) (INPUT_LIMIT = 2, :31,63-64). Cases follow the
 reference's lists (:146-330) at sizes the float64 oracle finishes quickly."""
+import os
+
 import numpy as np
 import pytest
 import torch
 
 from oracle import fa_bwd_oracle as bo
+from oracle import fa_oracle as orc
+from tests._util import assert_close_lse, assert_close_out, bits, odt
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 RTOL = ATOL = 1e-2
+NT = min(16, os.cpu_count() or 1)
 
 
 def rand_inputs(shape, dtype, g):
@@ -29,6 +35,18 @@ def check(name, got, ref):
     err = np.abs(got - ref)
     bad = err > ATOL + RTOL * np.abs(ref)
     assert not bad.any(), f"{name}: {int(bad.sum())} elements out of tolerance, max err {err.max():.3e}"
+
+
+def check_forward(out, lse, q, k, v, dtype, scale, causal, window, softcap, alibi=None, chunk=0, cu_q=None,
+                  cu_k=None):
+    """The forward the gradients start from (out, and the LSE the backward
+    recomputes P from) against the forward oracle, so an LSE error cannot
+    cancel out in the gradient check."""
+    ro, rl = orc.attention(bits(q), bits(k), bits(v), dtype=odt(dtype), scale=scale, softcap=softcap, causal=causal,
+                           window=window, alibi=alibi, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k,
+                           max_seqlen_q=None if cu_q is None else int(np.diff(cu_q).max()), nthreads=NT, chunk=chunk)
+    assert_close_out(out, ro, dtype)
+    assert_close_lse(lse, rl)
 
 
 def run_dense(dtype, B, H, Hk, Sq, Sk, D, causal, window=(-1, -1), softcap=0.0, alibi=False, api="v2", seed=0,
@@ -54,6 +72,8 @@ def run_dense(dtype, B, H, Hk, Sq, Sk, D, causal, window=(-1, -1), softcap=0.0, 
                                                      attention_chunk=chunk, return_attn_probs=True)
     dq, dk, dv = torch.autograd.grad(out, (qd, kd, vd), do.to(DEV))
     torch.cuda.synchronize()
+    check_forward(out, lse, q, k, v, dtype, scale, causal, window, softcap,
+                  alibi=None if slopes is None else slopes.numpy(), chunk=chunk)
     rq, rk, rv = bo.attention_bwd(q.float().numpy(), k.float().numpy(), v.float().numpy(), do.float().numpy(),
                                   lse.detach().cpu().numpy(), scale=scale, softcap=softcap, causal=causal,
                                   window=window, alibi=None if slopes is None else slopes.numpy(), chunk=chunk)
@@ -84,6 +104,7 @@ def run_varlen(dtype, H, Hk, lq, lk, D, causal, window=(-1, -1), softcap=0.0, ap
     out, lse = res[0], res[1]
     dq, dk, dv = torch.autograd.grad(out, (qd, kd, vd), do.to(DEV))
     torch.cuda.synchronize()
+    check_forward(out, lse, q, k, v, dtype, scale, causal, window, softcap, chunk=chunk, cu_q=cq, cu_k=ck)
     rq, rk, rv = bo.attention_bwd(q.float().numpy(), k.float().numpy(), v.float().numpy(), do.float().numpy(),
                                   lse.detach().cpu().numpy(), scale=scale, softcap=softcap, causal=causal,
                                   window=window, cu_seqlens_q=cq, cu_seqlens_k=ck, chunk=chunk)
@@ -258,3 +279,10 @@ def test_bwd_chunk(case):
 
 def test_bwd_varlen_chunk():
     run_varlen(torch.bfloat16, 4, 2, [130, 1, 260, 77], [130, 40, 300, 77], 128, True, api="v3", seed=9, chunk=96)
+
+
+@pytest.mark.parametrize("D", [111, 36])
+def test_bwd_v3_unaligned_headdim(D):
+    # the v3 API runs head dims that are not a multiple of 8 zero-padded; the
+    # gradients flow back through the padding
+    run_dense(torch.bfloat16, 2, 4, 2, 200, 260, D, True, api="v3", seed=30 + D)

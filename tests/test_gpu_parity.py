@@ -155,13 +155,13 @@ def test_decode_contiguous_append(dtype):
     run_kvcache(8, 1, 32, 8, 128, dtype, 2048, seqlens, s_new=1, causal=True, seed=5)
 
 
-@pytest.mark.parametrize("num_splits", [0, 1, 3])
-def test_decode_paged_split(num_splits):
-    print(f"case decode paged num_splits={num_splits}", flush=True)
+def test_decode_paged_split():
+    # the decode kernel's split over wave workers is decided on the device from
+    # cache_seqlens; num_splits is accepted and does not change it
+    print("case decode paged num_splits=3", flush=True)
     g = np.random.default_rng(6)
     seqlens = np.round(np.exp(g.uniform(np.log(16), np.log(3000), size=6))).astype(np.int32)
-    run_kvcache(6, 1, 64, 8, 128, torch.bfloat16, 0, seqlens, s_new=1, page=256, causal=True,
-                num_splits=num_splits, seed=6)
+    run_kvcache(6, 1, 64, 8, 128, torch.bfloat16, 0, seqlens, s_new=1, page=256, causal=True, num_splits=3, seed=6)
 
 
 def test_specverify_paged_window_alibi_batchidx():

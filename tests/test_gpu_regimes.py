@@ -2,9 +2,9 @@
 
 * BASELINE config 4 at its full size (B4, 2048 new tokens appended at 6144
   into an 8192-slot cache, H32/8, D128, bf16, NeoX rotary, causal): the
-  unsplit prefill path (about 100 key tiles per work item), once with
-  num_splits=1 and once with the automatic plan, against the CPU oracle on
-  two (batch, kv head) slices, and the whole cache bit for bit;
+  unsplit prefill path (about 100 key tiles per work item) with the
+  automatic plan, against the CPU oracle on four (batch, kv head) slices,
+  and the whole cache bit for bit;
 * the paged gather is bit-exact: a paged cache (permuted block table) and a
   contiguous cache with equal contents give identical out / LSE bits and
   identical cache contents after the append;
@@ -39,10 +39,10 @@ def _rope(n, rd, dtype, base=10000.0):
 
 
 # ---- BASELINE config 4 at full size --------------------------------------------------------------
-@pytest.mark.parametrize("num_splits", [1, 0])
-def test_c4_full_size_unsplit_prefill(num_splits):
+def test_c4_full_size_unsplit_prefill():
     import flash_attn_npu_v2
-    print(f"case c4 full size num_splits={num_splits}", flush=True)
+    num_splits = 0
+    print("case c4 full size (automatic plan: unsplit)", flush=True)
     B, S_new, L0, cap, H, Hk, D = 4, 2048, 6144, 8192, 32, 8, 128
     dtype = torch.bfloat16
     g = torch.Generator().manual_seed(404)
@@ -67,9 +67,11 @@ def test_c4_full_size_unsplit_prefill(num_splits):
     assert np.array_equal(bits(kc_d), rk), "k_cache after the append is not bit-exact"
     assert np.array_equal(bits(vc_d), rv), "v_cache after the append is not bit-exact"
 
-    # out / LSE on two (batch, kv head) slices: the first and the last work rows
+    # out / LSE on four (batch, kv head) slices of the 32, spread over the
+    # batches and kv heads (each slice holds all 32 row tiles of its pair,
+    # from the lightest, 6145 keys, to the heaviest, 8192)
     g_sz = H // Hk
-    for b, hk in ((0, 0), (3, 7)):
+    for b, hk in ((0, 0), (1, 3), (2, 4), (3, 7)):
         hs = slice(hk * g_sz, (hk + 1) * g_sz)
         ro, rl, _, _ = orc.kvcache_forward(
             bits(q[b:b + 1, :, hs]), bits(kc[b:b + 1, :, hk:hk + 1]), bits(vc[b:b + 1, :, hk:hk + 1]),
@@ -174,6 +176,34 @@ def test_append_ragged_q_with_empty_sequence():
     # sequence 1 has no query rows (no key tiles) but two new tokens
     run_v3(H=8, Hk=2, q_lens=[2, 0, 1], new_lens=[2] * 3, seqlens=[100, 37, 500], capacity=640, ragged_q=True,
            seed=542)
+
+
+@pytest.mark.parametrize("window", [(-1, -1), (8, 0)])
+def test_append_dense_empty_q(window):
+    """A (B, 0, H, D) q with new k / v: no attention runs, yet every new token
+    reaches the cache, with and without a left window."""
+    import flash_attn_npu_v2
+    print(f"case empty q with append, window {window}", flush=True)
+    B, H, Hk, D, cap, s_new = 3, 8, 2, 128, 64, 2
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(543)
+    L = np.array([5, 30, 61], np.int32)
+    q = torch.empty((B, 0, H, D), dtype=dtype)
+    kc = randn((B, cap, Hk, D), dtype, g, "cpu")
+    vc = randn((B, cap, Hk, D), dtype, g, "cpu")
+    kn = randn((B, s_new, Hk, D), dtype, g, "cpu")
+    vn = randn((B, s_new, Hk, D), dtype, g, "cpu")
+    kc_d, vc_d = kc.to(DEV), vc.to(DEV)
+    out, lse = flash_attn_npu_v2.flash_attn_with_kvcache(
+        q.to(DEV), kc_d, vc_d, k=kn.to(DEV), v=vn.to(DEV), cache_seqlens=torch.from_numpy(L).to(DEV), causal=True,
+        window_size=window, return_softmax_lse=True)
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (B, 0, H, D) and tuple(lse.shape) == (B, H, 0)
+    ek, ev = bits(kc).copy(), bits(vc).copy()
+    for b in range(B):
+        ek[b, L[b]:L[b] + s_new] = bits(kn)[b]
+        ev[b, L[b]:L[b] + s_new] = bits(vn)[b]
+    assert np.array_equal(bits(kc_d), ek) and np.array_equal(bits(vc_d), ev), "new tokens missing from the cache"
 
 
 # ---- a full cache: both append paths drop what does not fit ---------------------------------------

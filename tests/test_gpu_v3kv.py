@@ -211,3 +211,18 @@ def test_dense_chunk(case):
 
 def test_varlen_chunk():
     _dense_chunk(3, 130, 130, 8, 2, 128, torch.bfloat16, True, (-1, -1), 48, seed=12, varlen=True)
+
+
+# ---- head dims that are not a multiple of 8 (the v3 API runs them zero-padded) --------------------
+
+@pytest.mark.parametrize("D,page", [(111, 0), (111, 64), (36, 0)])
+def test_unaligned_headdim_decode_append(D, page):
+    rng = np.random.default_rng(600 + D + page)
+    run_v3(H=16, Hk=4, D=D, q_lens=[1] * 4, new_lens=[1] * 4, seqlens=rng.integers(20, 1900, 4), capacity=2048,
+           page=page, seed=600 + D + page)
+
+
+def test_unaligned_headdim_prefill_rotary_window():
+    rng = np.random.default_rng(610)
+    run_v3(H=8, Hk=2, D=111, q_lens=[70] * 3, new_lens=[70] * 3, seqlens=rng.integers(100, 900, 3), capacity=1024,
+           rotary="neox", rot_dim=96, window=(200, 0), seed=610)

@@ -61,3 +61,39 @@ def test_copy_is_checked_through_its_header():
         v3._metadata_for(bad, _call(), torch.device("cpu"))
     with pytest.raises(RuntimeError, match="uint8 tensor"):
         v3._metadata_for(torch.zeros(64, dtype=torch.int32), _call(), torch.device("cpu"))
+
+
+@pytest.mark.parametrize("B,H,Hk,D,maxq,page,splits", [
+    (64, 16, 4, 128, 64, 0, 0), (3, 16, 4, 128, 64, 0, 0), (3, 16, 4, 128, 64, 256, 0), (2, 32, 8, 256, 300, 0, 0),
+    (5, 8, 8, 64, 40, 0, 3), (1, 40, 8, 111, 90, 0, 0)])
+def test_workspace_covers_every_shorter_call(B, H, Hk, D, maxq, page, splits):
+    """A call of any query length up to max_seqlen_q, packed or not, fits the
+    planned workspace, also where a shorter call switches to the decode kernel
+    or to an automatic split over the key range (which need more scratch than
+    the call at max_seqlen_q)."""
+    md = v3.get_scheduler_metadata(B, maxq, 4096, H, Hk, D, cache_seqlens=torch.zeros(B, dtype=torch.int32),
+                                   page_size=page or None, num_splits=splits, causal=True)
+    d = md._fa_metadata
+    room = md.numel() - 256
+    for sq in range(1, maxq + 1):
+        for no_pack in (0, 1):
+            assert v3._workspace_at(d, sq, no_pack) <= room, (sq, no_pack)
+
+
+def test_workspace_short_decode_call_direct():
+    """The library planner itself, for a decode-sized call (Sq = 4) under
+    metadata planned at Sq = 64: the decode's partials fit."""
+    from fa_mi355x import capi
+    B, H, Hk, D = 64, 16, 4, 128
+    md = v3.get_scheduler_metadata(B, 64, 4096, H, Hk, D, cache_seqlens=torch.zeros(B, dtype=torch.int32),
+                                   causal=True)
+    dummy = 1 << 20
+    p = capi.new_params(dtype=1, batch=B, seqlen_q=4, nheads=H, nheads_k=Hk, headdim=D, headdim_v=D, q=dummy,
+                        q_batch_stride=4 * H * D, q_row_stride=H * D, q_head_stride=D, k=dummy,
+                        k_batch_stride=4096 * Hk * D, k_row_stride=Hk * D, k_head_stride=D, v=dummy,
+                        v_batch_stride=4096 * Hk * D, v_row_stride=Hk * D, v_head_stride=D, out=dummy,
+                        out_batch_stride=4 * H * D, out_row_stride=H * D, out_head_stride=D, softmax_lse=dummy,
+                        cache_seqlens=dummy, seqlen_k=4096, batch_cache=B, softmax_scale=1.0, is_causal=1)
+    st, need = capi.workspace_size(p, capi.FA_KIND_KVCACHE)
+    assert st == capi.FA_OK and need > 1 << 20
+    assert need <= md.numel() - 256

@@ -2,7 +2,9 @@
 scratch, for callers that cannot allocate) against fa_mha_fwd_kvcache with a
 caller workspace, both through the C ABI: two calls in a row, the second with
 a smaller input, each compared bit for bit (out, LSE and the cache after the
-append), and a call whose scratch need exceeds the limit is refused."""
+append), and a call whose scratch need exceeds the limit is refused; the
+calls leave device free memory unchanged and replay bitwise under HIP graph
+capture."""
 import ctypes
 
 import numpy as np
@@ -114,3 +116,42 @@ def test_noalloc_refuses_scratch_above_limit():
     st = L.fa_mha_fwd_kvcache_noalloc(ctypes.byref(p), torch.cuda.current_stream().cuda_stream)
     assert st == capi.FA_EWORKSPACE, (st, capi.last_error())
     assert "more than the" in capi.last_error()
+
+
+def test_noalloc_allocates_nothing_and_replays_under_graph_capture():
+    """The use the entry point is for: calls that allocate nothing, also when
+    captured into a HIP graph. Device free memory is unchanged by eager calls
+    (after a first call has loaded the kernels' code), and each replay of the
+    captured call, with eager work between replays, gives bitwise the eager
+    result (out and LSE cleared before each replay, so a replay that wrote
+    nothing would fail)."""
+    capi, L = _lib()
+    print("case noalloc: free memory around eager calls, graph capture and replays", flush=True)
+    rng = np.random.default_rng(960)
+    p, t = _decode_call(capi, 16, 32, 8, 128, 8192, rng.integers(1024, 8191, 16), seed=960)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        sh = side.cuda_stream
+        assert L.fa_mha_fwd_kvcache_noalloc(ctypes.byref(p), sh) == capi.FA_OK, capi.last_error()
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        for _ in range(3):
+            assert L.fa_mha_fwd_kvcache_noalloc(ctypes.byref(p), sh) == capi.FA_OK, capi.last_error()
+        torch.cuda.synchronize()
+        free1 = torch.cuda.mem_get_info()[0]
+    assert free1 == free0, f"device free memory changed by {free0 - free1} bytes over three calls"
+    ref = (bits(t["out"]), t["lse"].cpu().numpy().view(np.uint32), bits(t["kc"]), bits(t["vc"]))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        st = L.fa_mha_fwd_kvcache_noalloc(ctypes.byref(p), torch.cuda.current_stream().cuda_stream)
+    assert st == capi.FA_OK, capi.last_error()
+    for rep in range(3):
+        t["out"].zero_()
+        t["lse"].zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (bits(t["out"]), t["lse"].cpu().numpy().view(np.uint32), bits(t["kc"]), bits(t["vc"]))
+        for name, a, b in zip(("out", "lse", "k_cache", "v_cache"), got, ref):
+            assert np.array_equal(a, b), f"replay {rep}: {name} differs from the eager call"
