@@ -80,3 +80,25 @@ def test_opcheck_bwd():
     ov, lv = ops.varlen_fwd(qv, kv, kv, cu, cu, None, None, None, 50, 50, 0.0, 0.125, True, -1, 0, 0.0)
     _chk(ops.varlen_bwd, (randn((80, 8, 64), torch.bfloat16, g, DEV), qv, kv, kv, ov, lv, cu, cu, None, 50, 50, 0.0,
                           0.125, True, -1, 0, 0.0, False))
+
+
+def test_opcheck_fwd_with_metadata_workspace():
+    """The workspace a scheduler_metadata buffer brings in is written by the
+    kernels (split partials, the plan), so the schemas declare it mutable."""
+    from flash_attn_npu_v3 import interface as v3
+    print("case opcheck fwd / varlen_fwd / fwd_kvcache_v3 with a metadata workspace", flush=True)
+    g = torch.Generator().manual_seed(805)
+    q, k, v = randn((2, 40, 8, 128), torch.float16, g, DEV), randn((2, 50, 2, 128), torch.float16, g, DEV), \
+        randn((2, 50, 2, 128), torch.float16, g, DEV)
+    sl = torch.tensor([50, 50], dtype=torch.int32, device=DEV)
+    md = v3.get_scheduler_metadata(2, 40, 50, 8, 2, 128, sl, qkv_dtype=torch.float16, causal=True, num_splits=2)
+    ws = md[256:].clone()
+    _chk(ops.fwd, (q, k, v, None, 0.0, 0.088, True, -1, 0, 0.0), dict(num_splits=2, workspace=ws))
+    cu = torch.tensor([0, 30, 80], dtype=torch.int32, device=DEV)
+    qv, kv = randn((80, 8, 128), torch.float16, g, DEV), randn((80, 2, 128), torch.float16, g, DEV)
+    _chk(ops.varlen_fwd, (qv, kv, kv, cu, cu, None, None, None, 50, 50, 0.0, 0.088, True, -1, 0, 0.0),
+         dict(num_splits=2, workspace=ws))
+    kc, vc = randn((2, 64, 2, 128), torch.float16, g, DEV), randn((2, 64, 2, 128), torch.float16, g, DEV)
+    q1 = randn((2, 1, 8, 128), torch.float16, g, DEV)
+    _chk(ops.fwd_kvcache_v3, (q1, kc, vc, None, None, sl, None, None, None, None, None, None, None, None, 0, None,
+                              0.088, True, -1, 0, 0, 0.0, True, 0), dict(workspace=ws))
