@@ -409,9 +409,9 @@ def cpu_baseline(c, torch):
 def parity(c, ref, torch):
     """The GPU's result on the benchmarked inputs against the oracle's on the
     cpu_baseline sample: one more call on the first cache copy (the one the
-    oracle ran on), then out max-abs against the bf16 bar of 1e-2 (plus half
-    an ulp of the reference value: the oracle's output is itself rounded to
-    bf16), LSE relative error against 1e-4 (with a 1e-5 absolute floor for
+    oracle ran on), then out max-abs against the bf16 bar of 1e-2 (plus one
+    ulp of the reference value: both outputs are rounded to bf16 from their
+    fp32 values), LSE relative error against 1e-4 (with a 1e-5 absolute floor for
     |LSE| < 0.1), and the cache after the append bit for bit."""
     import numpy as np
     from fa_mi355x import capi
@@ -427,7 +427,7 @@ def parity(c, ref, torch):
     got = ref["sel_q"](out).float().cpu().numpy()
     want = orc.from_bits(ref["out"], orc.BF16).reshape(got.shape)
     err = np.abs(got - want)
-    out_ok = bool((err <= 1e-2 + np.abs(want) * 2.0 ** -8).all()) and not np.isnan(got).any()
+    out_ok = bool((err <= 1e-2 + np.abs(want) * 2.0 ** -7).all()) and not np.isnan(got).any()
     gl = ref["sel_q"](lse).cpu().numpy().astype(np.float64)
     rl = np.asarray(ref["lse"], dtype=np.float64).reshape(gl.shape)
     fin = np.isfinite(rl)

@@ -38,7 +38,7 @@ def check(out, lse, ref_o, ref_l, vmax=1.0):
     assert out.dtype == torch.bfloat16
     o = out.float().cpu().numpy()
     err = np.abs(o - ref_o)
-    tol = 1e-2 * vmax + np.abs(ref_o) * 2.0 ** -8
+    tol = 1e-2 * vmax + np.abs(ref_o) * 2.0 ** -7  # + one bf16 ulp (tests/_util.py ULP)
     assert (err <= tol).all(), f"out max err {err.max():.3e}"
     if lse is not None:
         l = lse.float().cpu().numpy()

@@ -179,7 +179,7 @@ def test_qv_dense_backward_vs_fp32_reference():
 # ---- pack_gqa = False ------------------------------------------------------------------------
 def _agree(packed, unpacked, dtype):
     """(out, lse) of the two layouts: out within the output tolerance plus
-    half an ulp of the value (both are rounded to 16 bits), lse within the
+    one ulp of the value (both are rounded to 16 bits), lse within the
     lse tolerance."""
     assert_close_out(unpacked[0], bits(packed[0]), dtype)
     assert_close_lse(unpacked[1], packed[1].float().cpu().numpy())

@@ -2,7 +2,7 @@
 (flash_attn_npu_v3 -> torch op -> C ABI) against the CPU oracle
 (oracle.fa_oracle.kvcache_forward_v3 / attention with chunk) on identical
 seeded inputs. Tolerances as everywhere: out max-abs 2e-3 (fp16) / 1e-2 (bf16)
-plus half an ulp of the reference value, LSE 1e-4 relative, the cache after
+plus one ulp of the reference value, LSE 1e-4 relative, the cache after
 the append bit-exact."""
 import os
 
