@@ -150,7 +150,11 @@ fa_status_t validate(const fa_fwd_params* p, int kind) {
     FA_CHECK(p->seqlen_k <= (1 << 30), "seqlen_k must be at most 2^30");
     FA_CHECK(p->block_table == nullptr || (int64_t)p->max_blocks_per_seq * p->page_block_size <= (int64_t)1 << 30,
              "block_table columns x page_block_size must be at most 2^30");
-    FA_CHECK(p->q && p->k && p->v && p->out && p->softmax_lse, "q, k, v, out and softmax_lse must be given");
+    // a call with no query rows (it may still append k / v) may pass empty,
+    // null q / out / softmax_lse, as zero-size tensors have no storage
+    const int64_t q_rows = p->cu_seqlens_q ? p->total_q : (int64_t)p->batch * p->seqlen_q;
+    FA_CHECK(p->k && p->v && (q_rows == 0 || (p->q && p->out && p->softmax_lse)),
+             "q, k, v, out and softmax_lse must be given");
     FA_CHECK(aligned16(p->q) && aligned16(p->k) && aligned16(p->v) && aligned16(p->out),
              "q, k, v and out must be 16-byte aligned");
     FA_CHECK(strides8(p->q_batch_stride, p->q_row_stride, p->q_head_stride), "q strides must be multiples of 8 elements");
@@ -406,7 +410,7 @@ fa_status_t run_forward_ws(const fa_fwd_params* p, int kind, void* stream_v, voi
         }
     }
     // no query rows: the append above is all the work
-    if (p->seqlen_q == 0 && kind != FA_KIND_VARLEN) {
+    if ((p->seqlen_q == 0 && kind != FA_KIND_VARLEN) || (p->cu_seqlens_q && p->total_q == 0)) {
         mark(1);
         mark(2);
         mark(3);

@@ -44,15 +44,18 @@ def randn(shape, dtype, gen, device):
 ULP = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
 
 
-def assert_close_out(out, ref_bits, dtype, tol=None):
+def assert_close_out(out, ref_bits, dtype, tol=None, rtol=0.0):
+    """|got - ref| <= tol + rtol * |ref| + one ulp of ref, elementwise; returns
+    the largest |got - ref|. rtol is 0 for the north-star bar."""
     tol = TOL[dtype] if tol is None else tol
     got = out.detach().float().cpu().numpy()
     ref = orc.from_bits(ref_bits, odt(dtype)).reshape(got.shape)
     err = np.abs(got - ref)
     mx = float(np.nanmax(err)) if err.size else 0.0
     assert not np.isnan(got).any(), "NaN in output"
-    excess = err - (tol + np.abs(ref) * ULP[dtype])
-    assert not (excess > 0).any(), f"out max-abs {mx:.3e} > {tol:.1e} + one ulp of the reference value"
+    excess = err - (tol + np.abs(ref) * (rtol + ULP[dtype]))
+    assert not (excess > 0).any(), (f"out max-abs {mx:.3e} > {tol:.1e} + {rtol:.0e} relative + one ulp of the "
+                                    f"reference value")
     return mx
 
 
