@@ -18,16 +18,29 @@ Checks: the oracle recomputes, per case, the first and the last sequence,
 each on its first and last kv head with all of that kv head's query heads
 (every sequence and head for the head-dim-111 cases), from the K / V rows of
 that sequence gathered on the host. LSE is held to the north-star 1e-4
-relative. The output is held to the bar these reference tests set for these
-inputs, |got - ref| <= 1e-2 + 1e-2 |ref| (torch.testing.assert_close with
-rtol = atol = 1e-2: tests/test_flash_attn_npu_v3.py:517-521,
-tests/test_flash_attn_npu_v2.py:404-407), plus one ulp of ref (both results
-are rounded to 16 bits), and the largest |got - ref| is printed. With values
-uniform in [-5, 5) the bf16 rounding of P before P.V (up to 2^-8 relative, at
-points that depend on each implementation's running maximum) can by itself
-move an output by up to 2^-8 * max|v| ~ 2e-2 in each of the two
-implementations, so the north-star's 1e-2 max-abs bar, set for the N(0, 1)
-BASELINE configs, is not a meaningful bar at this input range.
+relative. The output is checked twice:
+
+* against the oracle, at the north-star bar scaled to these inputs. Attention
+  is linear in v, so scaling v scales the output and every rounding error in
+  it (the 16-bit rounding of P before P.V, at points that depend on each
+  implementation's running maximum, and of the output itself) by the same
+  factor. The bar of 1e-2 (bf16) / 2e-3 (fp16) is stated for N(0, 1) values
+  (standard deviation 1); these lists draw v uniform in [-5, 5), standard
+  deviation 5 / sqrt(3), so the bar here is that many times the north-star
+  one (0.029 bf16, 0.0058 fp16), plus one ulp of the reference value (both
+  results are rounded to 16 bits);
+* against the exact result (float64, tests/golden/brute.py), at these
+  reference tests' own bar |got - exact| <= 1e-2 + 1e-2 |exact|
+  (torch.testing.assert_close with rtol = atol = 1e-2:
+  tests/test_flash_attn_npu_v3.py:517-521, tests/test_flash_attn_npu_v2.py:
+  404-407, where the reference compares with its golden, which rounds P at
+  the same 512-key stacks as its kernel).
+
+The first bar is looser than the reference's 1e-2 absolute for outputs near
+zero: two correct implementations that round P at different points differ by
+up to 2^-8 max|v| ~ 2e-2 each there (measured: kernel and oracle are both
+about 3e-3 from the exact result on average, at most 0.03 and 0.02). The
+second holds the kernel itself to the reference's bar.
 
 Window semantics are the small-op golden's (tests/fa_small_op_golden.py:21-58),
 which north_star names: after normalisation a negative bound of a local
@@ -43,12 +56,14 @@ import pytest
 import torch
 
 from oracle import fa_oracle as orc
-from tests._util import assert_close_lse, assert_close_out, bits, odt
+from tests.golden import brute
+from tests._util import TOL, assert_close_lse, assert_close_out, bits, odt
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 NT = min(16, os.cpu_count() or 1)
 F16, BF = torch.float16, torch.bfloat16
+SIGMA_V = 5.0 / math.sqrt(3.0)  # standard deviation of values uniform in [-5, 5)
 
 # (dtype, B, H, Hk, Sq, Sk, D, cache_mode, block, causal, wl, wr, softcap): the reference's v2 list
 V2_KV = [
@@ -274,13 +289,22 @@ def _unif(shape, dtype, gen):
 
 def _check(out_rows, lse_rows, q_rows, k_rows, v_rows, dtype, scale, causal, window, softcap):
     """One (sequence, kv head): out_rows (Sq, g, Dv) and lse_rows (g, Sq) from
-    the GPU against the oracle on q_rows (Sq, g, D), k_rows / v_rows (Lk, D)."""
+    the GPU against the oracle and the exact result on q_rows (Sq, g, D),
+    k_rows / v_rows (Lk, D)."""
     qh = bits(q_rows)[None]
     kh, vh = bits(k_rows)[None, :, None], bits(v_rows)[None, :, None]
     ro, rl = orc.attention(qh, kh, vh, dtype=odt(dtype), scale=scale, softcap=softcap, causal=causal,
                            window=window, nthreads=NT)
-    mx = assert_close_out(out_rows[None], ro, dtype, tol=1e-2, rtol=1e-2)
+    mx = assert_close_out(out_rows[None], ro, dtype, tol=TOL[dtype] * SIGMA_V)
     rel = assert_close_lse(lse_rows[None], rl) if lse_rows is not None else 0.0
+    ex, _ = brute.attention(q_rows.float().cpu().numpy(), k_rows.float().cpu().numpy()[:, None],
+                            v_rows.float().cpu().numpy()[:, None], scale, causal=causal, window=window,
+                            softcap=softcap)
+    got = out_rows.float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - ex)
+    bad = err > 1e-2 + 1e-2 * np.abs(ex)
+    assert not bad.any(), (f"{int(bad.sum())} outputs beyond 1e-2 + 1e-2 |exact| of the float64 result "
+                           f"(max err {err.max():.3e})")
     return mx, rel
 
 
