@@ -233,8 +233,12 @@ void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
     // kernel head dim: the prefill kernels come at 64, 128 and 256, the
     // decode kernel at 64 and 128; each serves the head dims up to its own
     // (the dims above the real ones read as zero); decode shapes above 128
-    // run on the prefill kernel
-    pl.decode = pl.rows_max <= kDecodeRows && p->headdim <= 128;
+    // run on the prefill kernel. A forced split count (num_splits >= 1) also
+    // runs on the prefill kernel, which cuts each sequence's keys into
+    // exactly that many chunks (1: none), as the reference's fixed split
+    // does (csrc/arch22/flash_attn_npu_v3/fa_split.h:335-402); the decode
+    // kernel's stream-K split is the heuristic one (num_splits = 0).
+    pl.decode = pl.rows_max <= kDecodeRows && p->headdim <= 128 && p->num_splits == 0;
     pl.kd = p->headdim <= 64 ? 64 : p->headdim <= 128 ? 128 : 256;
     pl.BM = pl.decode ? kDecodeRows : fa::fwd_tile_rows(pl.kd);
     pl.BN = pl.decode ? 32 : fa::fwd_tile_keys(pl.kd);

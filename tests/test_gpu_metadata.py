@@ -146,3 +146,37 @@ def test_flash_attn_kvcache_metadata_tnd():
     with pytest.raises(RuntimeError, match="different call"):
         flash_attn_with_kvcache(q.to(DEV), kc.to(DEV), vc.to(DEV), cache_seqlens=sl, page_table=bt.to(DEV),
                                 causal=True, scheduler_metadata=md)  # dense q against TND metadata
+
+
+@pytest.mark.parametrize("ns", [1, 3])
+def test_kvcache_decode_forced_split_count(ns):
+    """A forced num_splits on a decode-shaped call is honoured, as the
+    reference's fixed split is (csrc/arch22/flash_attn_npu_v3/fa_split.h:335-402):
+    the plan's per-sequence split count, read back from the metadata's
+    workspace, is ns for every sequence (a 2-key sequence included, whose third
+    chunk is empty), the append is bit-exact and the result is the oracle's."""
+    from flash_attn_npu_v3 import flash_attn_with_kvcache, get_scheduler_metadata
+    print(f"case kvcache decode forced num_splits={ns}", flush=True)
+    g = torch.Generator().manual_seed(710 + ns)
+    B, H, Hk, D, page, dt = 6, 64, 8, 128, 256, torch.bfloat16
+    L = np.array([16, 300, 3000, 1, 2047, 900], np.int32)
+    bt, kc, vc = _paged(B, L, page, Hk, D, dt, g, extra=1)
+    q = randn((B, 1, H, D), dt, g, "cpu")
+    kn, vn = randn((B, 1, Hk, D), dt, g, "cpu"), randn((B, 1, Hk, D), dt, g, "cpu")
+    sl = torch.from_numpy(L).to(DEV)
+    md = get_scheduler_metadata(B, 1, bt.shape[1] * page, H, Hk, D, sl, qkv_dtype=dt, page_size=page, causal=True,
+                                num_splits=ns)
+    kcd, vcd = kc.to(DEV), vc.to(DEV)
+    o, l, *_ = flash_attn_with_kvcache(q.to(DEV), kcd, vcd, k=kn.to(DEV), v=vn.to(DEV), cache_seqlens=sl,
+                                       page_table=bt.to(DEV), causal=True, return_softmax_lse=True, num_splits=ns,
+                                       scheduler_metadata=md)
+    torch.cuda.synchronize()
+    # the workspace starts with the plan table: B + 1 item offsets, then the
+    # split count of each sequence
+    sched = md[256:256 + 4 * (2 * B + 2)].cpu().numpy().view(np.int32)
+    assert (sched[B + 1:2 * B + 1] == ns).all(), sched
+    ro, rl, rk, rv = orc.kvcache_forward(bits(q), bits(kc), bits(vc), dtype=odt(dt), cache_seqlens=L, k=bits(kn),
+                                         v=bits(vn), block_table=bt.numpy(), causal=True, nthreads=NT)
+    assert np.array_equal(bits(kcd), rk) and np.array_equal(bits(vcd), rv), "append not bit-exact"
+    assert_close_out(o, ro, dt)
+    assert_close_lse(l, rl)

@@ -100,5 +100,6 @@ def test_opcheck_fwd_with_metadata_workspace():
          dict(num_splits=2, workspace=ws))
     kc, vc = randn((2, 64, 2, 128), torch.float16, g, DEV), randn((2, 64, 2, 128), torch.float16, g, DEV)
     q1 = randn((2, 1, 8, 128), torch.float16, g, DEV)
+    # the call's split count is the metadata's (2), as the v3 interface passes it
     _chk(ops.fwd_kvcache_v3, (q1, kc, vc, None, None, sl, None, None, None, None, None, None, None, None, 0, None,
-                              0.088, True, -1, 0, 0, 0.0, True, 0), dict(workspace=ws))
+                              0.088, True, -1, 0, 0, 0.0, True, 2), dict(workspace=ws))

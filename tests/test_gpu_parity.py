@@ -156,8 +156,8 @@ def test_decode_contiguous_append(dtype):
 
 
 def test_decode_paged_split():
-    # the decode kernel's split over wave workers is decided on the device from
-    # cache_seqlens; num_splits is accepted and does not change it
+    # a forced num_splits cuts every sequence's keys into that many chunks (the
+    # split prefill path) instead of the decode kernel's stream-K split
     print("case decode paged num_splits=3", flush=True)
     g = np.random.default_rng(6)
     seqlens = np.round(np.exp(g.uniform(np.log(16), np.log(3000), size=6))).astype(np.int32)
