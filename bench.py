@@ -445,10 +445,82 @@ def parity(c, ref, torch):
     return r
 
 
+# The matrix-core issue rate without memory: every wave runs chains of
+# independent bf16 MFMAs on register operands (8 accumulators of 16x16x32, or
+# 4 of 32x32x16), two waves per SIMD, one workgroup per CU.
+_MFMA_PROBE_SRC = r"""
+#include <hip/hip_runtime.h>
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+template <int KIND>
+__global__ void __launch_bounds__(512) mfma_probe(float* out, int iters, float seed) {
+    bf16x8 a, b;
+    for (int i = 0; i < 8; ++i) {
+        a[i] = (__bf16)(seed * (float)(threadIdx.x + i));
+        b[i] = (__bf16)(seed * (float)(i + 1));
+    }
+    float s = 0.f;
+    if constexpr (KIND == 0) {
+        f32x4 acc[8];
+        for (int j = 0; j < 8; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int it = 0; it < iters; ++it) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[j], 0, 0, 0);
+        }
+        for (int j = 0; j < 8; ++j) s += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+    } else {
+        f32x16 acc[4];
+        for (int j = 0; j < 4; ++j) acc[j] = f32x16{};
+        for (int it = 0; it < iters; ++it) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);
+        }
+        for (int j = 0; j < 4; ++j)
+            for (int e = 0; e < 16; ++e) s += acc[j][e];
+    }
+    out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+extern "C" int fa_mfma_probe(int kind, int blocks, int iters, float* out, void* stream) {
+    if (kind == 0) hipLaunchKernelGGL(mfma_probe<0>, dim3(blocks), dim3(512), 0, (hipStream_t)stream, out, iters, 1e-3f);
+    else hipLaunchKernelGGL(mfma_probe<1>, dim3(blocks), dim3(512), 0, (hipStream_t)stream, out, iters, 1e-3f);
+    return (int)hipGetLastError();
+}
+"""
+
+
+def mfma_rate(torch, hip, timed):
+    """bf16 TFLOP/s of the MFMA probe above (built here with hipcc, in a
+    temporary directory), 16x16x32 and 32x32x16."""
+    import subprocess
+    import tempfile
+    res = {}
+    with tempfile.TemporaryDirectory() as d:
+        src, lib = os.path.join(d, "mfma_probe.hip"), os.path.join(d, "mfma_probe.so")
+        with open(src, "w") as f:
+            f.write(_MFMA_PROBE_SRC)
+        subprocess.run(["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-O3", "-shared", "-fPIC", "-Xclang",
+                        "-target-feature", "-Xclang", "-packed-fp32-ops", src, "-o", lib], check=True,
+                       capture_output=True)
+        probe = ctypes.CDLL(lib)
+        probe.fa_mfma_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+        cus = torch.cuda.get_device_properties(0).multi_processor_count
+        out = torch.empty(cus * 512, dtype=torch.float32, device="cuda")
+        stream = torch.cuda.current_stream().cuda_stream
+        iters = 4000
+        for kind, name, flop in ((0, "mfma_16x16x32_bf16_tflops", 8 * 16384), (1, "mfma_32x32x16_bf16_tflops", 4 * 32768)):
+            def run():
+                if probe.fa_mfma_probe(kind, cus, iters, out.data_ptr(), stream) != 0:
+                    raise RuntimeError("MFMA probe launch failed")
+            t = timed(run, 5)
+            res[name] = round(cus * 8 * iters * flop / t / 1e12, 1)
+    return res
+
+
 def ceilings(torch, hip):
-    """Practical ceilings of this part, measured with library kernels: HBM
-    bandwidth of a 4 GiB device copy (read + write) and of a 4 GiB reduction
-    (read), and bf16 TFLOP/s of a large GEMM (torch.matmul, hipBLASLt)."""
+    """Practical ceilings of this part: HBM bandwidth of a 4 GiB device copy
+    (read + write) and of a 4 GiB reduction (read), bf16 TFLOP/s of a large
+    GEMM (torch.matmul, hipBLASLt) and of the MFMA issue rate alone."""
     stream = torch.cuda.current_stream().cuda_stream
     res = {}
 
@@ -478,7 +550,10 @@ def ceilings(torch, hip):
         torch.matmul(a, b, out=c)  # clock warm-up
     t = timed(lambda: torch.matmul(a, b, out=c), 50)
     res["gemm_bf16_tflops"] = round(2 * n ** 3 / t / 1e12, 1)
-    res["note"] = "4 GiB bf16 copy (2 x 4 GiB moved), torch.sum of 4 GiB bf16, 8192^3 bf16 torch.matmul"
+    del a, b, c
+    res.update(mfma_rate(torch, hip, timed))
+    res["note"] = ("4 GiB bf16 copy (2 x 4 GiB moved), torch.sum of 4 GiB bf16, 8192^3 bf16 torch.matmul, "
+                   "register-only bf16 MFMA chains (2 waves per SIMD, 8 x 16x16x32 or 4 x 32x32x16 per step)")
     torch.cuda.empty_cache()
     return res
 
