@@ -237,8 +237,10 @@ void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
     // runs on the prefill kernel, which cuts each sequence's keys into
     // exactly that many chunks (1: none), as the reference's fixed split
     // does (csrc/arch22/flash_attn_npu_v3/fa_split.h:335-402); the decode
-    // kernel's stream-K split is the heuristic one (num_splits = 0).
-    pl.decode = pl.rows_max <= kDecodeRows && p->headdim <= 128 && p->num_splits == 0;
+    // kernel's stream-K split is the heuristic one (num_splits = 0). Calls
+    // with qv stay on the decode kernel whatever num_splits says: only it
+    // forms the qv term.
+    pl.decode = pl.rows_max <= kDecodeRows && p->headdim <= 128 && (p->num_splits == 0 || p->qv != nullptr);
     pl.kd = p->headdim <= 64 ? 64 : p->headdim <= 128 ? 128 : 256;
     pl.BM = pl.decode ? kDecodeRows : fa::fwd_tile_rows(pl.kd);
     pl.BN = pl.decode ? 32 : fa::fwd_tile_keys(pl.kd);

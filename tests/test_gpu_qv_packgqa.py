@@ -95,11 +95,14 @@ def test_qv_kvcache_decode_vs_oracle(case):
     _kvcache_case(seed=500, **case)
 
 
-def test_qv_decode_with_alibi_through_the_op():
+@pytest.mark.parametrize("ns", [0, 3])
+def test_qv_decode_with_alibi_through_the_op(ns):
     # the v3 Python API has no alibi_slopes; the operator does (the decode
-    # kernel's qv instance forms its scores explicitly, ALiBi included)
+    # kernel's qv instance forms its scores explicitly, ALiBi included). A
+    # forced split count keeps a qv call on the decode kernel (only it forms
+    # the qv term).
     from fa_mi355x import ops
-    print("case qv decode + ALiBi (op)", flush=True)
+    print(f"case qv decode + ALiBi (op), num_splits={ns}", flush=True)
     g = torch.Generator().manual_seed(560)
     B, H, Hk, D, dtype = 3, 16, 4, 128, torch.bfloat16
     L = np.array([1200, 77, 600], np.int32)
@@ -112,7 +115,7 @@ def test_qv_decode_with_alibi_through_the_op():
                                           nthreads=NT)
     out, lse = ops.fwd_kvcache_v3(q.to(DEV), kc.to(DEV), vc.to(DEV), None, None, torch.from_numpy(L).to(DEV), None,
                                   None, None, None, None, slopes.to(DEV), None, None, 0, None, scale, True, -1, 0, 0,
-                                  0.0, True, 0, None, None, None, None, qv.to(DEV), None)
+                                  0.0, True, ns, None, None, None, None, qv.to(DEV), None)
     torch.cuda.synchronize()
     assert_close_out(out, ro, dtype)
     assert_close_lse(lse, rl)
