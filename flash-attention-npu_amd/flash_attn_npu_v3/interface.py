@@ -155,6 +155,10 @@ def _workspace_at(d, Sq, no_pack):
                                                  knew_head_stride=D, vnew_batch_stride=Hk * D,
                                                  vnew_row_stride=Hk * D, vnew_head_stride=D, rotary_cos=dummy,
                                                  rotary_sin=dummy, rotary_dim=16, seqlen_ro=Sk)))
+    if d["dtype"] != 3:
+        # a kvcache call with qv keeps the decode kernel's plan whatever num_splits says
+        cands.append((capi.FA_KIND_KVCACHE, dict(common, **kv, qv=dummy, qv_batch_stride=Sq * H * D,
+                                                 qv_row_stride=H * D, qv_head_stride=D)))
     if not page:
         cands.append((capi.FA_KIND_DENSE, dict(common, seqlen_k=Sk, batch_cache=B)))
     cands.append((capi.FA_KIND_VARLEN, dict(common, cu_seqlens_q=dummy, cu_seqlens_k=dummy, total_q=B * Sq,

@@ -97,3 +97,27 @@ def test_workspace_short_decode_call_direct():
     st, need = capi.workspace_size(p, capi.FA_KIND_KVCACHE)
     assert st == capi.FA_OK and need > 1 << 20
     assert need <= md.numel() - 256
+
+
+def test_workspace_forced_split_qv_decode_direct():
+    """A forced split count sends decode-sized calls to the split prefill path,
+    but a kvcache call with qv stays on the decode kernel (only it forms the qv
+    term) and keeps the decode's partials: metadata planned with num_splits=3
+    holds them (the library planner itself, asked for that call)."""
+    from fa_mi355x import capi
+    B, H, Hk, D, Sq = 1, 16, 4, 128, 4
+    md = v3.get_scheduler_metadata(B, Sq, 4096, H, Hk, D, cache_seqlens=torch.zeros(B, dtype=torch.int32),
+                                   num_splits=3, causal=True)
+    dummy = 1 << 20
+    kw = dict(dtype=1, batch=B, seqlen_q=Sq, nheads=H, nheads_k=Hk, headdim=D, headdim_v=D, q=dummy,
+              q_batch_stride=Sq * H * D, q_row_stride=H * D, q_head_stride=D, k=dummy,
+              k_batch_stride=4096 * Hk * D, k_row_stride=Hk * D, k_head_stride=D, v=dummy,
+              v_batch_stride=4096 * Hk * D, v_row_stride=Hk * D, v_head_stride=D, out=dummy,
+              out_batch_stride=Sq * H * D, out_row_stride=H * D, out_head_stride=D, softmax_lse=dummy,
+              cache_seqlens=dummy, seqlen_k=4096, batch_cache=B, softmax_scale=1.0, is_causal=1, num_splits=3)
+    st, plain = capi.workspace_size(capi.new_params(**kw), capi.FA_KIND_KVCACHE)
+    st2, with_qv = capi.workspace_size(capi.new_params(**kw, qv=dummy, qv_batch_stride=Sq * H * D,
+                                                       qv_row_stride=H * D, qv_head_stride=D), capi.FA_KIND_KVCACHE)
+    assert st == capi.FA_OK and st2 == capi.FA_OK
+    assert with_qv > plain  # the decode plan's partials, larger than the split prefill's here
+    assert with_qv <= md.numel() - 256
