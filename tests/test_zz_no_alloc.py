@@ -67,13 +67,13 @@ def _decode_call(capi, B, H, Hk, D, cap, seqlens, seed, page=0, num_splits=0, Sq
     return p, dict(q=q, kc=kc, vc=vc, kn=kn, vn=vn, sl=sl, out=out, lse=lse, bt=bt)
 
 
-def _run_pair(capi, L, shape, page, seed):
+def _run_pair(capi, L, shape, page, seed, num_splits=0):
     """The same call twice on separate copies of the caches: with a workspace,
     then without; returns both results."""
     stream = torch.cuda.current_stream().cuda_stream
     res = []
     for noalloc in (False, True):
-        p, t = _decode_call(capi, *shape, seed=seed, page=page)
+        p, t = _decode_call(capi, *shape, seed=seed, page=page, num_splits=num_splits)
         if noalloc:
             st = L.fa_mha_fwd_kvcache_noalloc(ctypes.byref(p), stream)
         else:
@@ -92,14 +92,18 @@ def test_noalloc_matches_workspace_entry_point():
     capi, L = _lib()
     rng = np.random.default_rng(900)
     # first call: config-2-like decode whose segments are cut across many
-    # wave workers (partials in the scratch); second: a smaller paged call
+    # wave workers (partials in the scratch); second: a smaller paged call;
+    # third: a decode with a forced split count, which runs the split prefill
+    # path (its sched table and partial rows in the scratch)
     shapes = [
-        (24, 32, 8, 128, 8192, rng.integers(1024, 8191, 24), 0),
-        (5, 64, 8, 128, 0, rng.integers(10, 3000, 5), 64),
+        (24, 32, 8, 128, 8192, rng.integers(1024, 8191, 24), 0, 0),
+        (5, 64, 8, 128, 0, rng.integers(10, 3000, 5), 64, 0),
+        (4, 32, 8, 128, 4096, rng.integers(500, 4000, 4), 0, 3),
     ]
-    for i, (B, H, Hk, D, cap, sl, page) in enumerate(shapes):
-        print(f"case noalloc call {i}: B{B} H{H}/{Hk} D{D} cap{cap} page{page}", flush=True)
-        (o0, l0, k0, v0), (o1, l1, k1, v1) = _run_pair(capi, L, (B, H, Hk, D, cap, sl), page, seed=900 + i)
+    for i, (B, H, Hk, D, cap, sl, page, ns) in enumerate(shapes):
+        print(f"case noalloc call {i}: B{B} H{H}/{Hk} D{D} cap{cap} page{page} num_splits{ns}", flush=True)
+        (o0, l0, k0, v0), (o1, l1, k1, v1) = _run_pair(capi, L, (B, H, Hk, D, cap, sl), page, seed=900 + i,
+                                                       num_splits=ns)
         assert np.array_equal(k0, k1) and np.array_equal(v0, v1), "caches differ after the append"
         assert np.array_equal(o0, o1), f"out differs in {(o0 != o1).sum()} elements"
         assert np.array_equal(l0, l1), f"lse differs in {(l0 != l1).sum()} elements"
