@@ -38,9 +38,13 @@ def _replay_and_check(fn, outs_eager, n=4):
             assert torch.equal(o, e), f"replay {rep} differs from the eager result"
 
 
-def test_graph_decode_with_append():
+@pytest.mark.parametrize("num_splits", [0, 3])
+def test_graph_decode_with_append(num_splits):
+    """num_splits 0: the decode kernel (append fused) and its merge; 3: a
+    forced split count, which runs the append kernel, the split prefill
+    kernel and its merge."""
     import flash_attn_npu_v2
-    print("case graph decode", flush=True)
+    print(f"case graph decode num_splits={num_splits}", flush=True)
     g = torch.Generator().manual_seed(70)
     B, H, Hk, D, cap = 8, 32, 8, 128, 2048
     q = _randn((B, 1, H, D), torch.bfloat16, g)
@@ -52,7 +56,7 @@ def test_graph_decode_with_append():
 
     def fn():
         return flash_attn_npu_v2.flash_attn_with_kvcache(q, kc, vc, k=kn, v=vn, cache_seqlens=seqlens, causal=True,
-                                                         return_softmax_lse=True)
+                                                         num_splits=num_splits, return_softmax_lse=True)
 
     eager = [t.clone() for t in fn()]
     torch.cuda.synchronize()
