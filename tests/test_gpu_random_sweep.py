@@ -1,0 +1,99 @@
+"""GPU parity over a seeded random sweep of kvcache and dense calls: shapes,
+head dims, GQA ratios, paging (page sizes on and off the fast path),
+cache_batch_idx, appends with and without rotary, causal / local windows,
+soft capping, ALiBi, forced split counts, both 16-bit dtypes and both APIs,
+each against the CPU oracle at the north-star bar (run_kvcache / run_dense).
+The list is drawn once from a fixed seed, so every run checks the same cases."""
+import numpy as np
+import pytest
+
+from tests.test_gpu_parity import run_dense, run_kvcache
+
+pytestmark = pytest.mark.gpu
+
+HEADS = [(4, 4), (8, 2), (16, 4), (32, 8), (12, 3), (6, 1)]
+DIMS = [64, 80, 96, 128, 128, 128, 192, 256]
+SQS = [1, 1, 1, 2, 3, 4, 5, 8, 16, 33, 100, 257]
+PAGES = [0, 0, 0, 16, 32, 64, 128, 256]
+
+
+def _kv_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        H, Hk = HEADS[rng.integers(len(HEADS))]
+        D = int(DIMS[rng.integers(len(DIMS))])
+        Sq = int(SQS[rng.integers(len(SQS))])
+        B = int(rng.integers(1, 9))
+        page = int(PAGES[rng.integers(len(PAGES))])
+        s_new = int(rng.choice([0, 0, 1, Sq]))
+        seqlens = [int(x) for x in rng.integers(0, int(rng.choice([600, 3000, 9000])), B)]
+        rotary = None
+        if s_new and rng.random() < 0.4:
+            # a rotary dim must be a multiple of 16 (as in Dao's kvcache rotary);
+            # "partial" rotates the first D / 2 dims
+            rotary = str(rng.choice(["neox", "interleaved", "partial"]))
+            if rotary == "partial" and (D // 2) % 16:
+                rotary = "neox"
+        causal = bool(rng.random() < 0.7)
+        window = (-1, -1)
+        r = rng.random()
+        if r < 0.25:
+            window = (int(rng.integers(0, 2000)), 0 if causal else int(rng.integers(0, 50)))
+        elif r < 0.35 and not causal:
+            window = (-1, int(rng.integers(0, 100)))
+        api = "v3" if rng.random() < 0.35 else "v2"
+        alibi = api == "v2" and rng.random() < 0.3
+        softcap = float(rng.choice([0.0, 0.0, 0.0, 30.0]))
+        batch_idx = bool(rng.random() < 0.25)
+        num_splits = int(rng.choice([0, 0, 0, 1, 3]))
+        dtype = str(rng.choice(["bf16", "fp16"]))
+        capacity = max(seqlens) + s_new + int(rng.integers(0, 64)) if not page else 0
+        cases.append(dict(B=B, Sq=Sq, H=H, Hk=Hk, D=D, dtype=dtype, capacity=capacity, seqlens=seqlens, s_new=s_new,
+                          page=page, rotary=rotary, causal=causal, window=window, alibi=alibi, batch_idx=batch_idx,
+                          num_splits=num_splits, softcap=softcap, seed=1000 + i, api=api))
+    return cases
+
+
+def _dense_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        H, Hk = HEADS[rng.integers(len(HEADS))]
+        D = int(DIMS[rng.integers(len(DIMS))])
+        B = int(rng.integers(1, 4))
+        Sq = int(rng.integers(1, 700))
+        Sk = int(rng.integers(1, 900))
+        causal = bool(rng.random() < 0.6)
+        window = (-1, -1)
+        if rng.random() < 0.3:
+            window = (int(rng.integers(0, 500)), 0 if causal else int(rng.integers(0, 200)))
+        cases.append(dict(B=B, Sq=Sq, Sk=Sk, H=H, Hk=Hk, D=D, dtype=str(rng.choice(["bf16", "fp16"])), causal=causal,
+                          window=window, softcap=float(rng.choice([0.0, 0.0, 20.0])),
+                          alibi=bool(rng.random() < 0.3), seed=2000 + i))
+    return cases
+
+
+KV_CASES = _kv_cases(200, 20251202)
+DENSE_CASES = _dense_cases(48, 20251203)
+
+
+def _dt(name):
+    import torch
+    return torch.bfloat16 if name == "bf16" else torch.float16
+
+
+@pytest.mark.parametrize("i", range(len(KV_CASES)))
+def test_random_kvcache(i):
+    c = dict(KV_CASES[i])
+    print(f"case random kvcache {i}: {c}", flush=True)
+    c["dtype"] = _dt(c["dtype"])
+    run_kvcache(**c)
+
+
+@pytest.mark.parametrize("i", range(len(DENSE_CASES)))
+def test_random_dense(i):
+    c = dict(DENSE_CASES[i])
+    print(f"case random dense {i}: {c}", flush=True)
+    c["dtype"] = _dt(c["dtype"])
+    run_dense(**c)
