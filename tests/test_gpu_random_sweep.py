@@ -97,3 +97,66 @@ def test_random_dense(i):
     print(f"case random dense {i}: {c}", flush=True)
     c["dtype"] = _dt(c["dtype"])
     run_dense(**c)
+
+
+# ---- v3 kvcache extensions: ragged q and new tokens, cache_leftpad, any page size,
+# rotary_seqlens, attention_chunk (run_v3 checks the caches bit for bit and the
+# output / LSE against the v3 oracle) --------------------------------------------------------------
+
+def _v3_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        H, Hk = HEADS[rng.integers(len(HEADS))]
+        D = int(rng.choice([64, 96, 128, 128, 256, 111, 36]))
+        B = int(rng.integers(1, 6))
+        decode = rng.random() < 0.5
+        q_lens = [int(x) for x in rng.integers(1, 5 if decode else 150, B)]
+        ragged_q = bool(rng.random() < 0.5)
+        if not ragged_q:
+            q_lens = [q_lens[0]] * B
+        ragged_new = bool(rng.random() < 0.4)
+        if ragged_new:
+            new_lens = [int(x) for x in rng.integers(0, 1 + max(q_lens), B)]
+        else:
+            new_lens = [int(rng.choice([0, 1, q_lens[0]]))] * B
+        seqlens = [int(x) for x in rng.integers(0, int(rng.choice([300, 2000, 6000])), B)]
+        page = int(rng.choice([0, 0, 1, 7, 16, 48, 64, 100, 256]))
+        leftpad = None
+        capacity = 0
+        if page == 0:
+            capacity = max(L + n for L, n in zip(seqlens, new_lens)) + 300
+            if rng.random() < 0.4:
+                leftpad = [int(x) for x in rng.integers(0, 300, B)]
+        rotary = rot_dim = rotary_seqlens = None
+        if max(new_lens) > 0 and rng.random() < 0.4:
+            rotary = str(rng.choice(["neox", "interleaved"]))
+            rot_dim = {111: 96, 36: 32}.get(D, D)
+            if rng.random() < 0.4:
+                rotary_seqlens = [int(x) for x in rng.integers(0, 500, B)]
+        causal = bool(rng.random() < 0.7)
+        window = (-1, -1)
+        chunk = 0
+        r = rng.random()
+        if r < 0.2:
+            window = (int(rng.integers(0, 1000)), 0 if causal else int(rng.integers(0, 40)))
+        elif r < 0.35:
+            chunk = int(rng.choice([32, 64, 100, 512]))
+        cases.append(dict(H=H, Hk=Hk, D=D, dtype=str(rng.choice(["bf16", "fp16"])), q_lens=q_lens, new_lens=new_lens,
+                          seqlens=seqlens, capacity=capacity, page=page, ragged_q=ragged_q, ragged_new=ragged_new,
+                          leftpad=leftpad, rotary=rotary, rot_dim=rot_dim, rotary_seqlens=rotary_seqlens,
+                          causal=causal, window=window, chunk=chunk, num_splits=int(rng.choice([0, 0, 1, 3])),
+                          seed=3000 + i))
+    return cases
+
+
+V3_CASES = _v3_cases(120, 20251204)
+
+
+@pytest.mark.parametrize("i", range(len(V3_CASES)))
+def test_random_v3_kvcache(i):
+    from tests.test_gpu_v3kv import run_v3
+    c = dict(V3_CASES[i])
+    print(f"case random v3 kvcache {i}: {c}", flush=True)
+    c["dtype"] = _dt(c["dtype"])
+    run_v3(**c)
