@@ -160,3 +160,52 @@ def test_random_v3_kvcache(i):
     print(f"case random v3 kvcache {i}: {c}", flush=True)
     c["dtype"] = _dt(c["dtype"])
     run_v3(**c)
+
+
+# ---- backward: dense and varlen gradients against the fp64 oracle, the forward
+# (out and LSE) against the forward oracle (run_dense / run_varlen of the
+# backward tests) ----------------------------------------------------------------------------------
+
+def _bwd_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        H, Hk = [(4, 4), (8, 2), (6, 1), (4, 1), (8, 8)][rng.integers(5)]
+        D = int(rng.choice([40, 64, 80, 96, 128, 128, 192, 256]))
+        api = "v3" if rng.random() < 0.35 else "v2"
+        causal = bool(rng.random() < 0.6)
+        window = (-1, -1)
+        chunk = 0
+        r = rng.random()
+        if r < 0.25:
+            window = (int(rng.integers(0, 300)), 0 if causal else int(rng.integers(0, 100)))
+        elif r < 0.4 and api == "v3":
+            chunk = int(rng.choice([32, 64, 100]))
+        softcap = float(rng.choice([0.0, 0.0, 30.0]))
+        alibi = api == "v2" and rng.random() < 0.25
+        dtype = str(rng.choice(["bf16", "fp16"]))
+        if rng.random() < 0.3:
+            B = int(rng.integers(1, 4))
+            lq = [int(x) for x in rng.integers(1, 300, B)]
+            lk = [int(x) for x in rng.integers(1, 300, B)]
+            cases.append(("varlen", dict(dtype=dtype, H=H, Hk=Hk, lq=lq, lk=lk, D=D, causal=causal, window=window,
+                                         softcap=softcap, api=api, seed=4000 + i, chunk=chunk)))
+        else:
+            cases.append(("dense", dict(dtype=dtype, B=int(rng.integers(1, 3)), H=H, Hk=Hk,
+                                        Sq=int(rng.integers(1, 400)), Sk=int(rng.integers(1, 400)), D=D,
+                                        causal=causal, window=window, softcap=softcap, alibi=alibi, api=api,
+                                        seed=4000 + i, chunk=chunk)))
+    return cases
+
+
+BWD_CASES = _bwd_cases(60, 20251205)
+
+
+@pytest.mark.parametrize("i", range(len(BWD_CASES)))
+def test_random_backward(i):
+    from tests import test_gpu_bwd as tb
+    kind, c = BWD_CASES[i]
+    c = dict(c)
+    print(f"case random backward {i}: {kind} {c}", flush=True)
+    c["dtype"] = _dt(c["dtype"])
+    (tb.run_varlen if kind == "varlen" else tb.run_dense)(**c)
