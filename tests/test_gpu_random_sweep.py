@@ -209,3 +209,96 @@ def test_random_backward(i):
     print(f"case random backward {i}: {kind} {c}", flush=True)
     c["dtype"] = _dt(c["dtype"])
     (tb.run_varlen if kind == "varlen" else tb.run_dense)(**c)
+
+
+# ---- FP8 (e4m3) forward: kvcache (contiguous or paged, decode- and prefill-shaped,
+# forced split counts) and dense calls with or without descales, against the FP8
+# oracle (exact widening, descaled scale, output times v_descale) ------------------------------------
+
+def _fp8_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        H, Hk = HEADS[rng.integers(len(HEADS))]
+        D = int(rng.choice([64, 96, 128, 128, 256]))
+        causal = bool(rng.random() < 0.7)
+        window = (-1, -1)
+        if rng.random() < 0.25:
+            window = (int(rng.integers(0, 800)), 0 if causal else int(rng.integers(0, 40)))
+        common = dict(H=H, Hk=Hk, D=D, causal=causal, window=window, softcap=float(rng.choice([0.0, 0.0, 30.0])),
+                      descale=bool(rng.random() < 0.8), seed=5000 + i)
+        if rng.random() < 0.7:
+            B = int(rng.integers(1, 6))
+            cases.append(("kvcache", dict(common, B=B, Sq=int(rng.choice([1, 1, 2, 4, 16, 100])),
+                                          L=[int(x) for x in rng.integers(1, int(rng.choice([500, 4000])), B)],
+                                          page=int(rng.choice([0, 0, 16, 48, 64, 256])),
+                                          num_splits=int(rng.choice([0, 0, 1, 3])))))
+        else:
+            cases.append(("dense", dict(common, B=int(rng.integers(1, 3)), Sq=int(rng.integers(1, 500)),
+                                        Sk=int(rng.integers(1, 700)))))
+    return cases
+
+
+FP8_CASES = _fp8_cases(60, 20251206)
+
+
+def _run_fp8(kind, B, H, Hk, D, causal, window, softcap, descale, seed, Sq, L=None, page=0, num_splits=0, Sk=0):
+    import torch
+    import flash_attn_npu_v3 as fa3
+    from oracle import fa_oracle as orc
+    from tests import test_gpu_fp8 as t8
+    g = torch.Generator().manual_seed(seed)
+    q = t8.fp8((B, Sq, H, D), g)
+    qd = kd = vd = None
+    if kind == "dense":
+        k, v = t8.fp8((B, Sk, Hk, D), g), t8.fp8((B, Sk, Hk, D), g)
+        if descale:
+            qd, kd, vd = t8.descales(B, Hk, g)
+        d = lambda x: None if x is None else x.to(t8.DEV)
+        out, lse = fa3.flash_attn_func(q.to(t8.DEV), k.to(t8.DEV), v.to(t8.DEV), causal=causal, window_size=window,
+                                       softcap=softcap, q_descale=d(qd), k_descale=d(kd), v_descale=d(vd),
+                                       return_attn_probs=True)
+        kx, vx, sk = t8.u8(k), t8.u8(v), None
+    else:
+        Lt = torch.tensor(L, dtype=torch.int32)
+        if page:
+            need = [(int(l) + page - 1) // page for l in L]
+            mb = max(need)
+            nblocks = sum(need) + 2
+            perm = torch.randperm(nblocks, generator=g)
+            bt = torch.zeros((B, mb), dtype=torch.int32)
+            o = 0
+            for b in range(B):
+                bt[b, :need[b]] = perm[o:o + need[b]]
+                o += need[b]
+            kc, vc = t8.fp8((nblocks, page, Hk, D), g), t8.fp8((nblocks, page, Hk, D), g)
+        else:
+            bt = None
+            cap = max(L) + 8
+            kc, vc = t8.fp8((B, cap, Hk, D), g), t8.fp8((B, cap, Hk, D), g)
+        if descale:
+            qd, kd, vd = t8.descales(B, Hk, g)
+        d = lambda x: None if x is None else x.to(t8.DEV)
+        out, lse, *_ = fa3.flash_attn_with_kvcache(q.to(t8.DEV), kc.to(t8.DEV), vc.to(t8.DEV), cache_seqlens=d(Lt),
+                                                   page_table=d(bt), q_descale=d(qd), k_descale=d(kd),
+                                                   v_descale=d(vd), causal=causal, window_size=window,
+                                                   softcap=softcap, num_splits=num_splits, return_softmax_lse=True)
+        if page:
+            kx = t8.u8(kc)[bt.numpy()].reshape(B, mb * page, Hk, D)
+            vx = t8.u8(vc)[bt.numpy()].reshape(B, mb * page, Hk, D)
+        else:
+            kx, vx = t8.u8(kc), t8.u8(vc)
+        sk = Lt.numpy()
+    torch.cuda.synchronize()
+    n = lambda x: None if x is None else x.numpy()
+    ro, rl = orc.attention_fp8(t8.u8(q), kx, vx, scale=D ** -0.5, q_descale=n(qd), k_descale=n(kd),
+                               v_descale=n(vd), causal=causal, window=window, softcap=softcap, seqlens_k=sk,
+                               nthreads=t8.NT)
+    t8.check(out, lse, ro, rl, vmax=1.0 if vd is None else float(vd.max()))
+
+
+@pytest.mark.parametrize("i", range(len(FP8_CASES)))
+def test_random_fp8(i):
+    kind, c = FP8_CASES[i]
+    print(f"case random fp8 {i}: {kind} {c}", flush=True)
+    _run_fp8(kind, **c)
