@@ -302,3 +302,46 @@ def test_random_fp8(i):
     kind, c = FP8_CASES[i]
     print(f"case random fp8 {i}: {kind} {c}", flush=True)
     _run_fp8(kind, **c)
+
+
+# ---- qv (scores add qv . v; decode-shaped kvcache calls, at most 16 packed rows
+# per kv head) and pack_gqa=False, against the v3 oracle ----------------------------------------------
+
+def _qv_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        H, Hk = HEADS[rng.integers(len(HEADS))]
+        g = H // Hk
+        D = int(rng.choice([64, 96, 128, 128]))
+        B = int(rng.integers(1, 6))
+        with_qv = bool(rng.random() < 0.6)
+        smax = max(1, 16 // g) if with_qv else 40
+        ragged = None
+        Sq = int(rng.integers(1, smax + 1))
+        if rng.random() < 0.3:
+            ragged = [int(x) for x in rng.integers(1, smax + 1, B)]
+        L = [int(x) for x in rng.integers(0, int(rng.choice([500, 3000])), B)]
+        page = int(rng.choice([0, 0, 16, 64, 256]))
+        new = int(rng.choice([0, 0, 1])) if ragged is None else 0
+        capacity = 0 if page else max(L) + new + 16
+        window = (-1, -1)
+        if rng.random() < 0.25:
+            window = (int(rng.integers(0, 600)), 0)
+        cases.append(dict(B=B, Sq=Sq, H=H, Hk=Hk, D=D, dtype=str(rng.choice(["bf16", "fp16"])), L=L,
+                          capacity=capacity, page=page, new=new, window=window, ragged=ragged,
+                          pack_gqa=None if with_qv and rng.random() < 0.5 else False, seed=6000 + i,
+                          with_qv=with_qv, softcap=float(rng.choice([0.0, 0.0, 5.0]))))
+    return cases
+
+
+QV_CASES = _qv_cases(48, 20251207)
+
+
+@pytest.mark.parametrize("i", range(len(QV_CASES)))
+def test_random_qv_pack_gqa(i):
+    from tests.test_gpu_qv_packgqa import _kvcache_case
+    c = dict(QV_CASES[i])
+    print(f"case random qv / pack_gqa {i}: {c}", flush=True)
+    c["dtype"] = _dt(c["dtype"])
+    _kvcache_case(**c)
