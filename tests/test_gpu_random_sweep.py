@@ -345,3 +345,78 @@ def test_random_qv_pack_gqa(i):
     print(f"case random qv / pack_gqa {i}: {c}", flush=True)
     c["dtype"] = _dt(c["dtype"])
     _kvcache_case(**c)
+
+
+# ---- scheduler_metadata: a kvcache call given get_scheduler_metadata's plan
+# (made for max_seqlen_q, the call may be shorter) gives bit for bit the result
+# of the same call without it: the plan and workspace it carries cover the call ----------------------
+
+def _md_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        H, Hk = HEADS[rng.integers(len(HEADS))]
+        maxq = int(rng.choice([1, 2, 4, 8, 16, 64, 200]))
+        causal = bool(rng.random() < 0.7)
+        window = (-1, -1)
+        if rng.random() < 0.25:
+            window = (int(rng.integers(0, 1000)), 0 if causal else int(rng.integers(0, 40)))
+        B = int(rng.integers(1, 9))
+        cases.append(dict(B=B, H=H, Hk=Hk, D=int(rng.choice([64, 128, 128, 256])), maxq=maxq,
+                          Sq=int(rng.integers(1, maxq + 1)), L=[int(x) for x in rng.integers(0, 4000, B)],
+                          page=int(rng.choice([0, 0, 16, 64, 256])), s_new=int(rng.choice([0, 0, 1])),
+                          causal=causal, window=window, softcap=float(rng.choice([0.0, 0.0, 10.0])),
+                          num_splits=int(rng.choice([0, 0, 1, 3])), pack_gqa=[None, False][int(rng.random() < 0.3)],
+                          dtype=str(rng.choice(["bf16", "fp16"])), seed=7000 + i))
+    return cases
+
+
+MD_CASES = _md_cases(60, 20251208)
+
+
+@pytest.mark.parametrize("i", range(len(MD_CASES)))
+def test_random_scheduler_metadata(i):
+    import torch
+    from flash_attn_npu_v3 import flash_attn_with_kvcache, get_scheduler_metadata
+    from tests._util import bits, randn
+    c = MD_CASES[i]
+    print(f"case random scheduler metadata {i}: {c}", flush=True)
+    dt = _dt(c["dtype"])
+    B, H, Hk, D, Sq, page, s_new = c["B"], c["H"], c["Hk"], c["D"], c["Sq"], c["page"], c["s_new"]
+    g = torch.Generator().manual_seed(c["seed"])
+    L = np.asarray(c["L"], np.int32)
+    if page:
+        need = [(int(x) + s_new + page - 1) // page for x in L]
+        nb = sum(need) + 3
+        perm = torch.randperm(nb, generator=g).to(torch.int32)
+        bt = torch.zeros((B, max(max(need), 1)), dtype=torch.int32)
+        o = 0
+        for b in range(B):
+            bt[b, :need[b]] = perm[o:o + need[b]]
+            o += need[b]
+        kc, vc = randn((nb, page, Hk, D), dt, g, "cpu"), randn((nb, page, Hk, D), dt, g, "cpu")
+        max_k = bt.shape[1] * page
+    else:
+        bt = None
+        max_k = int(L.max()) + s_new + 8
+        kc, vc = randn((B, max_k, Hk, D), dt, g, "cpu"), randn((B, max_k, Hk, D), dt, g, "cpu")
+    q = randn((B, Sq, H, D), dt, g, "cpu")
+    kn = vn = None
+    if s_new:
+        kn, vn = randn((B, s_new, Hk, D), dt, g, "cpu"), randn((B, s_new, Hk, D), dt, g, "cpu")
+    sl = torch.from_numpy(L).to("cuda")
+    md = get_scheduler_metadata(B, c["maxq"], max_k, H, Hk, D, sl, qkv_dtype=dt, page_size=page or None,
+                                max_seqlen_k_new=s_new, causal=c["causal"], window_size=c["window"],
+                                has_softcap=c["softcap"] > 0, num_splits=c["num_splits"], pack_gqa=c["pack_gqa"])
+    res = []
+    for use in (True, False):
+        kcd, vcd = kc.to("cuda"), vc.to("cuda")
+        d = lambda x: None if x is None else x.to("cuda")
+        o, lse, *_ = flash_attn_with_kvcache(d(q), kcd, vcd, k=d(kn), v=d(vn), cache_seqlens=sl, page_table=d(bt),
+                                             causal=c["causal"], window_size=c["window"], softcap=c["softcap"],
+                                             num_splits=c["num_splits"], pack_gqa=c["pack_gqa"],
+                                             return_softmax_lse=True, scheduler_metadata=md if use else None)
+        torch.cuda.synchronize()
+        res.append((bits(o), lse.cpu().numpy().view(np.uint32), bits(kcd), bits(vcd)))
+    for a, b in zip(*res):
+        assert np.array_equal(a, b), "the call with scheduler_metadata differs from the call without it"
