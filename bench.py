@@ -517,6 +517,152 @@ def mfma_rate(torch, hip, timed):
     return res
 
 
+# A read-only copy of the decode kernel's loads: the same tile list (32-key
+# tiles of every (sequence, kv head) segment, visible keys only), the same
+# per-lane 16-byte chunks (16 key rows x 64 contiguous bytes per load
+# instruction), 4 waves per CU with an equal split of the tiles, 3 tiles in
+# flight, no compute (an xor of every load). Its time is the rate HBM gives
+# that access pattern, the decode kernel's own ceiling.
+_DECODE_READ_SRC = r"""
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int MAXB = 64, HKM = 8;
+struct RdArgs {
+    const uint16_t* k; const uint16_t* v; const int* bt; long long bt_stride; int nblocks, page;
+    const int* pref; const int* lot; const int* sk; const int* crow; int B, Hk;
+    long long sb, si, sh; u32x4* sink;
+};
+__global__ void __launch_bounds__(256, 1) decode_read(RdArgs a) {
+    __shared__ int s_pref[MAXB + 1], s_lot[MAXB], s_sk[MAXB], s_crow[MAXB];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, G = lane >> 4;
+    if (tid <= a.B) s_pref[tid] = a.pref[tid];
+    if (tid < a.B) { s_lot[tid] = a.lot[tid]; s_sk[tid] = a.sk[tid]; s_crow[tid] = a.crow[tid]; }
+    __syncthreads();
+    const int T = s_pref[a.B];
+    const long long W = (long long)gridDim.x * 4, wid = (long long)wave * gridDim.x + blockIdx.x;
+    const int t0 = (int)(wid * T / W), t1 = (int)((wid + 1) * T / W);
+    u32x4 kr[3][2][4], vr[3][2][4];
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    auto issue = [&](int t, u32x4 (&kk)[2][4], u32x4 (&vv)[2][4]) {
+        if (t >= t1) return;
+        int bl = 0, bh = a.B;
+        while (bh - bl > 1) { const int m = (bl + bh) >> 1; if (s_pref[m] <= t) bl = m; else bh = m; }
+        const int per = (s_pref[bl + 1] - s_pref[bl]) / a.Hk, o = t - s_pref[bl];
+        const int hk = o / per, j = o % per, sk = s_sk[bl];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            int key = (s_lot[bl] + j) * 32 + h * 16 + li;
+            key = key < sk ? key : sk - 1;
+            long long off;
+            if (a.bt) {
+                int blk = a.bt[(long long)s_crow[bl] * a.bt_stride + key / a.page];
+                blk = blk < 0 ? 0 : (blk >= a.nblocks ? a.nblocks - 1 : blk);
+                off = (long long)blk * a.sb + (long long)(key % a.page) * a.si + (long long)hk * a.sh;
+            } else {
+                off = (long long)s_crow[bl] * a.sb + (long long)key * a.si + (long long)hk * a.sh;
+            }
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                kk[h][s] = *reinterpret_cast<const u32x4*>(a.k + off + 8 * (4 * s + G));
+                vv[h][s] = *reinterpret_cast<const u32x4*>(a.v + off + 8 * (4 * s + G));
+            }
+        }
+    };
+    issue(t0, kr[0], vr[0]);
+    issue(t0 + 1, kr[1], vr[1]);
+    for (int tb = t0; tb < t1; tb += 3) {
+#pragma unroll
+        for (int st = 0; st < 3; ++st) {
+            const int t = tb + st;
+            if (t < t1) {
+                issue(t + 2, kr[(st + 2) % 3], vr[(st + 2) % 3]);
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) acc ^= kr[st][h][s] ^ vr[st][h][s];
+            }
+        }
+    }
+    a.sink[wid * 64 + lane] = acc;
+}
+extern "C" int fa_decode_read(const RdArgs* a, int grid, void* stream) {
+    if (a->B > MAXB) return 1;
+    hipLaunchKernelGGL(decode_read, dim3(grid), dim3(256), 0, (hipStream_t)stream, *a);
+    return (int)hipGetLastError();
+}
+"""
+
+
+class _RdArgs(ctypes.Structure):
+    _fields_ = [("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("bt", ctypes.c_void_p),
+                ("bt_stride", ctypes.c_longlong), ("nblocks", ctypes.c_int), ("page", ctypes.c_int),
+                ("pref", ctypes.c_void_p), ("lot", ctypes.c_void_p), ("sk", ctypes.c_void_p),
+                ("crow", ctypes.c_void_p), ("B", ctypes.c_int), ("Hk", ctypes.c_int),
+                ("sb", ctypes.c_longlong), ("si", ctypes.c_longlong), ("sh", ctypes.c_longlong),
+                ("sink", ctypes.c_void_p)]
+
+
+def decode_read_ceiling(torch, hip, timed):
+    """Microseconds per call of the read-only copy of the decode kernel's loads
+    above on the inputs of configs c2 and c5 (the same caches, rotated the same
+    way), against the decode kernel's own attention time on them."""
+    import subprocess
+    import tempfile
+    res = {}
+    with tempfile.TemporaryDirectory() as d:
+        src, lib = os.path.join(d, "decode_read.hip"), os.path.join(d, "decode_read.so")
+        with open(src, "w") as f:
+            f.write(_DECODE_READ_SRC)
+        subprocess.run(["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-O3", "-shared", "-fPIC", "-Xclang",
+                        "-target-feature", "-Xclang", "-packed-fp32-ops", src, "-o", lib], check=True,
+                       capture_output=True)
+        probe = ctypes.CDLL(lib)
+        probe.fa_decode_read.argtypes = [ctypes.POINTER(_RdArgs), ctypes.c_int, ctypes.c_void_p]
+        cus = torch.cuda.get_device_properties(0).multi_processor_count
+        stream = torch.cuda.current_stream().cuda_stream
+        sink = torch.empty(cus * 4 * 64 * 4, dtype=torch.int32, device="cuda")
+        for name, ncopy in (("c2", 2), ("c5", 4)):
+            c = build_case(name, torch, "cuda", ncopy)
+            q, kn, vn, caches, bt, bidx = c["keep"][:6]
+            B, Hk, Sq = c["B"], c["Hk"], c["Sq"]
+            L = [int(x) for x in c["L"]]
+            if name == "c2":
+                sk, lo = [x + 1 for x in L], [0] * B          # the cached keys and the appended one
+                crow = list(range(B))
+            else:
+                sk, lo = L, [max(0, x - Sq - 4096) for x in L]  # the union of the 4 rows' windows
+                crow = [int(x) for x in bidx.cpu()]
+            lot = [x // 32 for x in lo]
+            pref = [0]
+            for b in range(B):
+                pref.append(pref[-1] + Hk * ((sk[b] + 31) // 32 - lot[b]))
+            ints = {n_: torch.tensor(v_, dtype=torch.int32, device="cuda")
+                    for n_, v_ in (("pref", pref), ("lot", lot), ("sk", sk), ("crow", crow))}
+            args = []
+            for kc, vc in caches:
+                assert kc.stride() == vc.stride() and kc.shape[-1] == 128
+                a = _RdArgs(k=kc.data_ptr(), v=vc.data_ptr(), bt=0 if bt is None else bt.data_ptr(),
+                            bt_stride=0 if bt is None else bt.stride(0), nblocks=kc.shape[0],
+                            page=kc.shape[1] if bt is not None else 1, pref=ints["pref"].data_ptr(),
+                            lot=ints["lot"].data_ptr(), sk=ints["sk"].data_ptr(), crow=ints["crow"].data_ptr(),
+                            B=B, Hk=Hk, sb=kc.stride(0), si=kc.stride(1), sh=kc.stride(2), sink=sink.data_ptr())
+                args.append(a)
+            state = {"i": 0}
+
+            def run():
+                a = args[state["i"] % len(args)]
+                state["i"] += 1
+                if probe.fa_decode_read(ctypes.byref(a), cus, stream) != 0:
+                    raise RuntimeError("decode read probe launch failed")
+            t = timed(run, 40)
+            res[f"decode_read_only_{name}_us"] = round(t * 1e6, 1)
+            res[f"decode_read_only_{name}_tbps"] = round(c["attn_bytes"] / t / 1e12, 3)
+            del c, args, ints
+            torch.cuda.empty_cache()
+    return res
+
+
 def ceilings(torch, hip):
     """Practical ceilings of this part: HBM bandwidth of a 4 GiB device copy
     (read + write) and of a 4 GiB reduction (read), bf16 TFLOP/s of a large
@@ -552,8 +698,11 @@ def ceilings(torch, hip):
     res["gemm_bf16_tflops"] = round(2 * n ** 3 / t / 1e12, 1)
     del a, b, c
     res.update(mfma_rate(torch, hip, timed))
+    res.update(decode_read_ceiling(torch, hip, timed))
     res["note"] = ("4 GiB bf16 copy (2 x 4 GiB moved), torch.sum of 4 GiB bf16, 8192^3 bf16 torch.matmul, "
-                   "register-only bf16 MFMA chains (2 waves per SIMD, 8 x 16x16x32 or 4 x 32x32x16 per step)")
+                   "register-only bf16 MFMA chains (2 waves per SIMD, 8 x 16x16x32 or 4 x 32x32x16 per step), "
+                   "a read-only copy of the decode kernel's loads on the c2 and c5 inputs (TB/s of their "
+                   "algorithmic attention bytes)")
     torch.cuda.empty_cache()
     return res
 
