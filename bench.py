@@ -520,8 +520,9 @@ def mfma_rate(torch, hip, timed):
 # A read-only copy of the decode kernel's loads: the same tile list (32-key
 # tiles of every (sequence, kv head) segment, visible keys only), the same
 # per-lane 16-byte chunks (16 key rows x 64 contiguous bytes per load
-# instruction), 4 waves per CU with an equal split of the tiles, 3 tiles in
-# flight, no compute (an xor of every load). Its time is the rate HBM gives
+# instruction), 4 waves per CU with an equal split of the tiles, the two waves
+# of a pair streaming two adjacent kv heads of one range when the kv head count
+# is even, 3 tiles in flight, no compute (an xor of every load). Its time is the rate HBM gives
 # that access pattern, the decode kernel's own ceiling.
 _DECODE_READ_SRC = r"""
 #include <hip/hip_runtime.h>
@@ -540,16 +541,20 @@ __global__ void __launch_bounds__(256, 1) decode_read(RdArgs a) {
     if (tid < a.B) { s_lot[tid] = a.lot[tid]; s_sk[tid] = a.sk[tid]; s_crow[tid] = a.crow[tid]; }
     __syncthreads();
     const int T = s_pref[a.B];
-    const long long W = (long long)gridDim.x * 4, wid = (long long)wave * gridDim.x + blockIdx.x;
-    const int t0 = (int)(wid * T / W), t1 = (int)((wid + 1) * T / W);
+    // the decode kernel's worker groups: with an even kv head count a pair of
+    // waves takes one tile range of head groups, each wave one head of the pair
+    const int hs = (a.Hk % 2) == 0 ? 2 : 1, hsel = wave % hs;
+    const long long W = (long long)gridDim.x * (4 / hs), gw = (long long)(wave / hs) * gridDim.x + blockIdx.x;
+    const long long wid = gw * hs + hsel;
+    const int t0 = (int)(gw * T / W), t1 = (int)((gw + 1) * T / W);
     u32x4 kr[3][2][4], vr[3][2][4];
     u32x4 acc = {0u, 0u, 0u, 0u};
     auto issue = [&](int t, u32x4 (&kk)[2][4], u32x4 (&vv)[2][4]) {
         if (t >= t1) return;
         int bl = 0, bh = a.B;
         while (bh - bl > 1) { const int m = (bl + bh) >> 1; if (s_pref[m] <= t) bl = m; else bh = m; }
-        const int per = (s_pref[bl + 1] - s_pref[bl]) / a.Hk, o = t - s_pref[bl];
-        const int hk = o / per, j = o % per, sk = s_sk[bl];
+        const int per = (s_pref[bl + 1] - s_pref[bl]) / (a.Hk / hs), o = t - s_pref[bl];
+        const int hk = (o / per) * hs + hsel, j = o % per, sk = s_sk[bl];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             int key = (s_lot[bl] + j) * 32 + h * 16 + li;
@@ -634,9 +639,10 @@ def decode_read_ceiling(torch, hip, timed):
                 sk, lo = L, [max(0, x - Sq - 4096) for x in L]  # the union of the 4 rows' windows
                 crow = [int(x) for x in bidx.cpu()]
             lot = [x // 32 for x in lo]
-            pref = [0]
+            pref = [0]  # tile prefix over (sequence, kv head group)
+            groups = Hk // 2 if Hk % 2 == 0 else Hk
             for b in range(B):
-                pref.append(pref[-1] + Hk * ((sk[b] + 31) // 32 - lot[b]))
+                pref.append(pref[-1] + groups * ((sk[b] + 31) // 32 - lot[b]))
             ints = {n_: torch.tensor(v_, dtype=torch.int32, device="cuda")
                     for n_, v_ in (("pref", pref), ("lot", lot), ("sk", sk), ("crow", crow))}
             args = []

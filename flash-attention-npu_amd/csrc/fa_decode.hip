@@ -9,7 +9,9 @@
 //   * The work list is every 32-key tile of every (sequence, kv head)
 //     "segment", built in LDS from cache_seqlens by each workgroup (no host
 //     round trip). The tiles are cut into equal contiguous ranges, one per
-//     wave ("worker"), so uneven sequence lengths still balance exactly.
+//     wave ("worker"), so uneven sequence lengths still balance exactly; with
+//     an even kv head count the two waves of a pair on one CU share a range
+//     and stream two adjacent kv heads of it (dec_hs below).
 //   * A worker streams its tiles with a STAGES-deep register pipeline of
 //     16-byte loads (K straight into MFMA operand layout, V through a
 //     wave-private LDS tile read back transposed), so each wave keeps up to
@@ -66,6 +68,17 @@ struct DecCfg {
     static __device__ __forceinline__ int vswz(int r, int c) { return HD == 64 ? swz_v64(r, c) : (c ^ (r & 15)); }
 };
 
+// Heads per worker group: with an even kv head count, the two waves of a pair
+// (waves 0, 1 and 2, 3 of a workgroup, so one CU) stream kv heads 2g and 2g + 1
+// of the same sequence over the same tile range, so the CU requests the two
+// adjacent 256-byte pieces of each key row together. Measured (one box,
+// alternating): c2 attention 118.4-119.3 -> 116.3 us, c3 301.2-302.9 -> 297.0-
+// 297.6 us, c5 39.7-40.2 -> 39.1-39.2 us, c3f8 unchanged; a read-only copy of
+// the loads reads c2's bytes in 112-113 us against 115-116 us.
+// The tile list and the split then run over head groups: group g of sequence b
+// holds that sequence's tiles once, each wave of the pair takes its head.
+__device__ __forceinline__ int dec_hs(const FwdArgs& a) { return (a.Hk % 2) == 0 ? 2 : 1; }
+
 struct DecSeg {
     int S, n;         // first global tile, tiles
     int b, hk;
@@ -105,7 +118,9 @@ __device__ __forceinline__ void dec_batch(const FwdArgs& a, int b, DecBatch& d, 
     ntiles = (sq > 0 && hi > lo) ? (hi + KT - 1) / KT - d.lo_tile : 0;
 }
 
-__device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref, const DecBatch* s_b, int t) {
+// segment of group tile t for head h of the group (hs heads per group)
+__device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref, const DecBatch* s_b, int t, int hs,
+                                             int h) {
     int bl = 0, bh = a.B;
     while (bh - bl > 1) {
         int mid = (bl + bh) >> 1;
@@ -113,11 +128,12 @@ __device__ __forceinline__ DecSeg dec_seg_of(const FwdArgs& a, const int* s_pref
     }
     DecSeg s;
     s.b = bl;
-    const int per = (s_pref[bl + 1] - s_pref[bl]) / a.Hk;
+    const int per = (s_pref[bl + 1] - s_pref[bl]) / (a.Hk / hs);
     s.n = per;
     const int o = t - s_pref[bl];
-    s.hk = per > 0 ? o / per : 0;
-    s.S = s_pref[bl] + s.hk * per;
+    const int hg = per > 0 ? o / per : 0;
+    s.hk = hg * hs + h;
+    s.S = s_pref[bl] + hg * per;
     s.kvh = a.kvdiv == 1 ? s.hk : s.hk / a.kvdiv;
     const DecBatch d = s_b[bl];
     s.lo_tile = d.lo_tile;
@@ -182,7 +198,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         int nt;
         dec_batch<KT>(a, b, d, nt);
         s_bat[b] = d;
-        s_pref[b + 1] = a.Hk * nt;
+        s_pref[b + 1] = (a.Hk / dec_hs(a)) * nt;
     }
     __syncthreads();
     if (wave == 0) {
@@ -209,18 +225,21 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
         for (int b = tid; b <= a.B; b += 256) a.sched[b] = s_pref[b];
 
     const long long T = s_pref[a.B];
-    const long long W = (long long)gridDim.x * NWAVE;
+    const int hs = dec_hs(a), hgs = a.Hk / hs;  // heads per group, groups per sequence
+    const int hsel = wave % hs;                   // this wave's head within its group
+    const long long W = (long long)gridDim.x * (NWAVE / hs);  // group workers
     // workers are numbered wave-major: the 4 waves of a CU take tile ranges a
     // quarter of the tile list apart instead of 4 neighbouring ones, so they
     // do not stream neighbouring addresses of one (sequence, kv head) at the
     // same time (c2 attention 124.0 -> 120.4 us, c3 319.7 -> 312.4 us, c2f8
     // 76.6 -> 72.1 us on one box)
-    const long long wid = (long long)wave * gridDim.x + blockIdx.x;
+    const long long gw = (long long)(wave / hs) * gridDim.x + blockIdx.x;
+    const long long wid = gw * hs + hsel;  // this wave's partial slots
     // tiles [t0, t1) of this worker: the split by cost of fa_decode_split.h
-    const long long ovh = seg_ovh(T, W, (long long)a.B * a.Hk);
-    const long long CT = split_total(T, ovh, a.B, a.Hk);
-    const int t0 = split_tfirst(wid * CT / W, s_pref, a.B, a.Hk, ovh, T, CT);
-    const int t1 = split_tfirst((wid + 1) * CT / W, s_pref, a.B, a.Hk, ovh, T, CT);
+    const long long ovh = seg_ovh(T, W, (long long)a.B * hgs);
+    const long long CT = split_total(T, ovh, a.B, hgs);
+    const int t0 = split_tfirst(gw * CT / W, s_pref, a.B, hgs, ovh, T, CT);
+    const int t1 = split_tfirst((gw + 1) * CT / W, s_pref, a.B, hgs, ovh, T, CT);
     FA_PHASE(ph_plan = __builtin_amdgcn_s_memrealtime(); if (t0 >= t1) ph_write(wid, 0);)
     if (t0 >= t1) return;  // no block barrier follows: waves are independent from here
 
@@ -238,7 +257,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
             const int t = base + i;
             int blk = 0;
             if (t < t1) {
-                DecSeg s = dec_seg_of(a, s_pref, s_bat, t);
+                DecSeg s = dec_seg_of(a, s_pref, s_bat, t, hs, hsel);
                 const int key0 = (s.lo_tile + (t - s.S)) * KT;
                 const int pidx = a.page_shift >= 0 ? key0 >> a.page_shift : key0 / a.page;
                 blk = a.block_table[(int64_t)s.crow * a.bt_stride + pidx];
@@ -252,7 +271,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     // ---- issue side: STAGES-deep register pipeline ------------------------------------
     u32x4 kr[STAGES][NH][KL], vr[STAGES][NH][KL];
     int bk[STAGES];  // paged block id of each in-flight tile
-    DecSeg is = dec_seg_of(a, s_pref, s_bat, t0);
+    DecSeg is = dec_seg_of(a, s_pref, s_bat, t0, hs, hsel);
 
     auto row_ptr = [&](const ET* base, int64_t sb, int64_t si, int64_t sh, const DecSeg& s, int key,
                        int blk) -> const ET* {
@@ -281,7 +300,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
 
     auto issue = [&](int t, u32x4 (&kk)[NH][KL], u32x4 (&vv)[NH][KL], int& blk) {
         if (t >= t1) return;
-        if (t >= is.S + is.n) is = dec_seg_of(a, s_pref, s_bat, t);
+        if (t >= is.S + is.n) is = dec_seg_of(a, s_pref, s_bat, t, hs, hsel);
         blk = 0;
         if (tab_ok) {
             if (t >= tab_base + TABN) {
@@ -324,7 +343,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
     };
 
     // ---- compute side --------------------------------------------------------------------
-    DecSeg cs = dec_seg_of(a, s_pref, s_bat, t0);
+    DecSeg cs = dec_seg_of(a, s_pref, s_bat, t0, hs, hsel);
     u32x4 qreg[KSTEPS];
     u32x4 qvreg[QV ? KSTEPS : 1];  // QV: the qv row
     u32x4 q8[2];  // FP8: the raw q bytes of dims G * D / 4 .. + D / 4 (zero-padded to 32)
@@ -618,7 +637,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                       bk[(st + STAGES - 1) % STAGES]);
                 if (t >= cs.S + cs.n) {
                     end_seg(cs);
-                    cs = dec_seg_of(a, s_pref, s_bat, t);
+                    cs = dec_seg_of(a, s_pref, s_bat, t, hs, hsel);
                     begin_seg(cs);
                     FA_PHASE(++ph_nseg;)
                 }
@@ -657,21 +676,23 @@ __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int wor
     constexpr int CH = D / DSPLIT / 8;   // 8-dim chunks per row in one workgroup
     const int sig = blockIdx.x / DSPLIT, dsl = blockIdx.x % DSPLIT;
     const int b = sig / a.Hk, hk = sig % a.Hk;
+    const int hs = dec_hs(a), hgs = a.Hk / hs, hg = hk / hs, hsel = hk % hs;
+    const long long sigg = (long long)b * hgs + hg;  // the segment's head group
     if (b >= a.B) return;
     int sq = a.cu_seqlens_q ? a.cu_seqlens_q[b + 1] - a.cu_seqlens_q[b] : a.Sq;
     sq = min(max(sq, 0), a.Sq);
     const int rows = sq * a.g;
     if (rows <= 0) return;
     const long long T = a.sched[a.B];
-    const int per = (a.sched[b + 1] - a.sched[b]) / a.Hk;
-    const long long S = a.sched[b] + (long long)hk * per;
-    const long long W = workers;
+    const int per = (a.sched[b + 1] - a.sched[b]) / hgs;
+    const long long S = a.sched[b] + (long long)hg * per;   // the group's first tile
+    const long long W = workers / hs;                        // group workers
     const int tid = threadIdx.x;
     // the split of the decode kernel (fa_decode_split.h): tile t of segment j
     // costs t + ovh * j, and worker w owns the costs [w * CT / W, (w + 1) * CT / W)
-    const long long ovh = seg_ovh(T, W, (long long)a.B * a.Hk);
-    const long long CT = split_total(T, ovh, a.B, a.Hk);
-    auto owner = [&](long long t) { return split_owner(t + ovh * sig, W, CT); };  // t in this segment
+    const long long ovh = seg_ovh(T, W, (long long)a.B * hgs);
+    const long long CT = split_total(T, ovh, a.B, hgs);
+    auto owner = [&](long long t) { return split_owner(t + ovh * sigg, W, CT); };  // t in this group
     long long wf = 0;
     int n = 0;
     if (per > 0) {
@@ -685,14 +706,14 @@ __global__ void __launch_bounds__(256) fa_decode_merge_kernel(FwdArgs a, int wor
     bool first_slot1 = false;
     if (per > 0 && S > 0) {
         // that tile's segment only matters through its cost, so only when ovh > 0
-        const long long jp = ovh > 0 ? split_prev_segment(b, hk, a.Hk, a.sched) : 0;
+        const long long jp = ovh > 0 ? split_prev_segment(b, hg, hgs, a.sched) : 0;
         first_slot1 = split_owner(S - 1 + ovh * jp, W, CT) == wf;
     }
     // partial j of this segment -> its first partial row
     auto prow0 = [&](int j) -> long long {
         const long long w = T >= W ? wf + j : owner(S + j);
         const int slot = (j == 0 && first_slot1) ? 1 : 0;
-        return (w * 2 + slot) * 16;
+        return ((w * hs + hsel) * 2 + slot) * 16;
     };
     // ---- one pass: each of NG thread groups folds its share of the partials
     // with a running maximum (lse and O of a partial are loaded together), then
