@@ -520,9 +520,9 @@ def mfma_rate(torch, hip, timed):
 # A read-only copy of the decode kernel's loads: the same tile list (32-key
 # tiles of every (sequence, kv head) segment, visible keys only), the same
 # per-lane 16-byte chunks (16 key rows x 64 contiguous bytes per load
-# instruction), 4 waves per CU with an equal split of the tiles, the two waves
-# of a pair streaming two adjacent kv heads of one range when the kv head count
-# is even, 3 tiles in flight, no compute (an xor of every load). Its time is the rate HBM gives
+# instruction), 4 waves per CU with an equal split of the tiles, the waves of
+# a CU streaming adjacent kv heads of one range (4 heads when the kv head count
+# is a multiple of 4, else 2 when it is even), 3 tiles in flight, no compute (an xor of every load). Its time is the rate HBM gives
 # that access pattern, the decode kernel's own ceiling.
 _DECODE_READ_SRC = r"""
 #include <hip/hip_runtime.h>
@@ -541,9 +541,9 @@ __global__ void __launch_bounds__(256, 1) decode_read(RdArgs a) {
     if (tid < a.B) { s_lot[tid] = a.lot[tid]; s_sk[tid] = a.sk[tid]; s_crow[tid] = a.crow[tid]; }
     __syncthreads();
     const int T = s_pref[a.B];
-    // the decode kernel's worker groups: with an even kv head count a pair of
-    // waves takes one tile range of head groups, each wave one head of the pair
-    const int hs = (a.Hk % 2) == 0 ? 2 : 1, hsel = wave % hs;
+    // the decode kernel's worker groups: the 4 (or 2) waves of a group take one
+    // tile range of kv head groups, each wave one head of the group
+    const int hs = (a.Hk % 4) == 0 ? 4 : ((a.Hk % 2) == 0 ? 2 : 1), hsel = wave % hs;
     const long long W = (long long)gridDim.x * (4 / hs), gw = (long long)(wave / hs) * gridDim.x + blockIdx.x;
     const long long wid = gw * hs + hsel;
     const int t0 = (int)(gw * T / W), t1 = (int)((gw + 1) * T / W);
@@ -640,7 +640,7 @@ def decode_read_ceiling(torch, hip, timed):
                 crow = [int(x) for x in bidx.cpu()]
             lot = [x // 32 for x in lo]
             pref = [0]  # tile prefix over (sequence, kv head group)
-            groups = Hk // 2 if Hk % 2 == 0 else Hk
+            groups = Hk // 4 if Hk % 4 == 0 else (Hk // 2 if Hk % 2 == 0 else Hk)
             for b in range(B):
                 pref.append(pref[-1] + groups * ((sk[b] + 31) // 32 - lot[b]))
             ints = {n_: torch.tensor(v_, dtype=torch.int32, device="cuda")

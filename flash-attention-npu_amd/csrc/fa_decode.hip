@@ -9,9 +9,9 @@
 //   * The work list is every 32-key tile of every (sequence, kv head)
 //     "segment", built in LDS from cache_seqlens by each workgroup (no host
 //     round trip). The tiles are cut into equal contiguous ranges, one per
-//     wave ("worker"), so uneven sequence lengths still balance exactly; with
-//     an even kv head count the two waves of a pair on one CU share a range
-//     and stream two adjacent kv heads of it (dec_hs below).
+//     wave ("worker"), so uneven sequence lengths still balance exactly; the
+//     waves of one CU share a range and stream adjacent kv heads of it when
+//     the kv head count allows (4 heads per CU, else 2; dec_hs below).
 //   * A worker streams its tiles with a STAGES-deep register pipeline of
 //     16-byte loads (K straight into MFMA operand layout, V through a
 //     wave-private LDS tile read back transposed), so each wave keeps up to
@@ -68,16 +68,19 @@ struct DecCfg {
     static __device__ __forceinline__ int vswz(int r, int c) { return HD == 64 ? swz_v64(r, c) : (c ^ (r & 15)); }
 };
 
-// Heads per worker group: with an even kv head count, the two waves of a pair
-// (waves 0, 1 and 2, 3 of a workgroup, so one CU) stream kv heads 2g and 2g + 1
-// of the same sequence over the same tile range, so the CU requests the two
-// adjacent 256-byte pieces of each key row together. Measured (one box,
-// alternating): c2 attention 118.4-119.3 -> 116.3 us, c3 301.2-302.9 -> 297.0-
-// 297.6 us, c5 39.7-40.2 -> 39.1-39.2 us, c3f8 unchanged; a read-only copy of
-// the loads reads c2's bytes in 112-113 us against 115-116 us.
+// Heads per worker group: when the kv head count is a multiple of 4, the 4
+// waves of a workgroup (one CU) stream kv heads 4g .. 4g + 3 of the same
+// sequence over the same tile range, so the CU requests the 4 adjacent
+// head pieces of each key row together (1 KiB for bf16 at head dim 128); with
+// an even count that is not, waves 0, 1 and 2, 3 form such groups of 2.
+// Measured (one box, alternating runs, attention us): one head per wave ->
+// pairs, c2 118.4-119.3 -> 116.3, c3 301.2-302.9 -> 297.0-297.6, c5 39.7-40.2
+// -> 39.1-39.2, c3f8 unchanged; pairs -> 4 heads, c2 119.0-119.5 -> 115.4-115.9,
+// c3 297.8-298.3 -> 295.2-295.5, c5 39.3-39.5 -> 39.4-39.8, c3f8 172.9-173.0 ->
+// 173.5-173.7.
 // The tile list and the split then run over head groups: group g of sequence b
-// holds that sequence's tiles once, each wave of the pair takes its head.
-__device__ __forceinline__ int dec_hs(const FwdArgs& a) { return (a.Hk % 2) == 0 ? 2 : 1; }
+// holds that sequence's tiles once, each wave of the group takes its head.
+__device__ __forceinline__ int dec_hs(const FwdArgs& a) { return (a.Hk % 4) == 0 ? 4 : ((a.Hk % 2) == 0 ? 2 : 1); }
 
 struct DecSeg {
     int S, n;         // first global tile, tiles

@@ -10,9 +10,9 @@
 // pref[B] = T).
 //
 // The kernels call these functions with kv head GROUPS in place of kv heads:
-// with an even kv head count a group is two adjacent heads streamed together
-// by a pair of waves, so Hk here is the group count Hk / 2 and W the count of
-// wave pairs. The split itself does not depend on what a segment holds.
+// a group is 4 (or 2) adjacent heads streamed together by the 4 (or 2) waves
+// of one CU, so Hk here is the group count and W the count of wave groups.
+// The split itself does not depend on what a segment holds.
 //
 // Static split by cost: a worker that moves to another segment pays about a
 // tile's time for it (the q reload and the store of the finished segment).
