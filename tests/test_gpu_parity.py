@@ -359,15 +359,41 @@ def test_decode_large_paged_uneven():
 
 
 def test_decode_many_segments_cost_split():
-    # 64 x 8 = 512 (sequence, kv head) segments over 1024 wave workers with at
-    # least 16 tiles each: the regime of BASELINE config 3, where the decode
-    # split counts every segment as one extra tile and a worker's first
+    # 64 x 8 = 512 (sequence, kv head) segments over 1024 waves, in the
+    # kernel's groups of 4 kv heads 128 group segments over 256 wave groups,
+    # with at least 16 tiles each: the regime of BASELINE config 3, where the
+    # decode split counts every segment as one extra tile and a worker's first
     # partial and latest whole output are held until it ends
     print("case decode many segments (split by cost)", flush=True)
     rng = np.random.default_rng(35)
     seqlens = np.round(np.exp(rng.uniform(np.log(512), np.log(8192), size=64))).astype(np.int64)
     assert 64 * 8 * int(np.mean(seqlens)) // 32 >= 16 * 1024
     run_kvcache(64, 1, 64, 8, 128, torch.bfloat16, 0, seqlens, s_new=1, page=256, causal=True, seed=35)
+
+
+# ---- kv head groups: the 4 waves of a CU stream 4 adjacent kv heads of one tile range when
+# nheads_k % 4 == 0, pairs of waves 2 heads when it is otherwise even, else one head each; the
+# tile split and the merge of the partials run over those groups
+@pytest.mark.parametrize("Hk", [1, 2, 3, 4, 6, 12, 16])
+@pytest.mark.parametrize("page", [0, 64])
+@pytest.mark.parametrize("Sq", [1, 4])
+def test_decode_kv_head_groups(Hk, page, Sq):
+    print(f"case decode kv head groups Hk={Hk} page={page} Sq={Sq}", flush=True)
+    rng = np.random.default_rng(40 + Hk)
+    seqlens = rng.integers(1, 6000, size=6)
+    seqlens[:3] = [1, 33, 5999]
+    run_kvcache(6, Sq, 2 * Hk, Hk, 128, torch.bfloat16, 0 if page else 6144, seqlens, s_new=Sq, page=page,
+                causal=True, seed=40 + Hk)
+
+
+@pytest.mark.parametrize("Hk,B", [(6, 96), (12, 48)])
+def test_decode_kv_head_groups_cost_split(Hk, B):
+    # groups of 2 (Hk 6) and 4 (Hk 12) kv heads with at least half a group
+    # segment and 16 tiles per wave group on a 256-CU part: the split by cost
+    print(f"case decode kv head groups cost split Hk={Hk} B={B}", flush=True)
+    rng = np.random.default_rng(50 + Hk)
+    seqlens = rng.integers(1000, 3000, size=B)
+    run_kvcache(B, 1, 2 * Hk, Hk, 128, torch.bfloat16, 0, seqlens, s_new=1, page=64, causal=True, seed=50 + Hk)
 
 
 def test_decode_one_long_sequence():
