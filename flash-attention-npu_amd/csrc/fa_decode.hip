@@ -663,9 +663,11 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
 // per segment, each on D / DSPLIT dims of the head; a segment with no visible key
 // gets out = 0, lse = +inf): per row, lse = M + ln(sum_j exp(lse_j - M)) and
 // O = sum_j exp(lse_j - lse) * O_j (the closed form of
-// CombineScale.hpp:150-194). The partial list of a segment [S, S+n) is known
-// from the worker split alone: workers owner(S)..owner(S+n-1) when every
-// worker has a tile (T >= W), else one worker per tile. NG thread groups each
+// CombineScale.hpp:150-194). The partial list of a segment is known from the
+// worker split alone: the tiles [S, S+n) of its kv head group belong to group
+// workers owner(S)..owner(S+n-1) when every group worker has a tile (T >= W),
+// else one group worker per tile, and within a group worker the wave of this
+// kv head (hk % hs) wrote the head's partials. NG thread groups each
 // fold a share of the partials in one pass with a running maximum (the lse
 // and O of a partial are loaded together), and the groups are combined in
 // LDS. (Merging inside the decode kernel, by the last wave to finish a
