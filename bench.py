@@ -758,7 +758,7 @@ def bench_bwd(torch, hip, steps, warmup):
     flops = 2.5 * 4 * D * pairs * B * H
     return {"us_per_call": us, "flops_per_call": flops, "tflops_call": flops / (us * 1e-6) / 1e12,
             "frac_mfma": flops / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,
-            "workload": f"backward, dense causal B{B} S{S} H{H}/{Hk} D{D} bf16 (dsum + dK/dV + dQ kernels)"}
+            "workload": f"backward, dense causal B{B} S{S} H{H}/{Hk} D{D} bf16 (dQ with dsum, then dK/dV kernels)"}
 
 
 TRAFFIC_PROFILES = ("profiles/fa_attention_kernels_hbm_traffic.txt", "profiles/fa_decode_kernel_fp8_hbm_traffic.txt")

@@ -11,8 +11,10 @@
 //   dQ = dS K,      dK = dS^T Q
 // (the golden's rowsum(dP * P) equals dsum up to the rounding of out).
 //
-// MI355X design: three launches, no atomics, so results are deterministic.
-//   * fa_bwd_dsum_kernel: dsum per (row, head), also returned as softmax_d.
+// MI355X design: two launches, no atomics, so results are deterministic.
+//   * fa_bwd_dq_kernel runs first and also computes dsum for its rows (from
+//     the out rows and the dout rows it loads anyway), writing it for the
+//     dK/dV kernel and as the returned softmax_d.
 //   * fa_bwd_dkdv_kernel: one workgroup per (batch, kv head, 128-key block);
 //     each of 8 waves keeps 16 keys' K and V in registers as MFMA B operands
 //     and streams the packed (query, head) rows of all g query heads through
@@ -138,47 +140,6 @@ __device__ __forceinline__ float bw_score(const BwdArgs& a, float x, float slope
         t = 0.f;
         return x * a.scale_log2;
     }
-}
-
-// ---- dsum = rowsum(dout * out) -------------------------------------------------------------
-// One 16-lane group per (token, head) row over up to 256 dims (16 dims per lane).
-__global__ void __launch_bounds__(256) fa_bwd_dsum_kernel(BwdArgs a, int dt) {
-    const int grp = threadIdx.x >> 4, l16 = threadIdx.x & 15;
-    const int64_t row = (int64_t)blockIdx.x * 16 + grp;  // token * H + head
-    const int64_t ntok = a.cu_seqlens_q ? (int64_t)a.total_q : (int64_t)a.B * a.Sq;
-    if (row >= ntok * a.H) return;
-    const int h = (int)(row % a.H);
-    const int64_t tok = row / a.H;
-    int64_t oo, od, lo;
-    if (a.cu_seqlens_q) {
-        oo = tok * a.o_si + (int64_t)h * a.o_sh;
-        od = tok * a.do_si + (int64_t)h * a.do_sh;
-        lo = (int64_t)h * a.lse_sh + tok;
-    } else {
-        const int64_t b = tok / a.Sq, i = tok % a.Sq;
-        oo = b * a.o_sb + i * a.o_si + (int64_t)h * a.o_sh;
-        od = b * a.do_sb + i * a.do_si + (int64_t)h * a.do_sh;
-        lo = b * a.lse_sb + (int64_t)h * a.lse_sh + i;
-    }
-    const uint16_t* o = static_cast<const uint16_t*>(a.out) + oo;
-    const uint16_t* d = static_cast<const uint16_t*>(a.dout) + od;
-    float acc = 0.f;
-    for (int c = l16; c * 8 < a.hd; c += 16) {
-        const u32x4 ov = *reinterpret_cast<const u32x4*>(o + c * 8);
-        const u32x4 dv = *reinterpret_cast<const u32x4*>(d + c * 8);
-        uint16_t oh[8], dh[8];
-        __builtin_memcpy(oh, &ov, 16);
-        __builtin_memcpy(dh, &dv, 16);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float x = dt == DT_BF16 ? f16_to_32<DT_BF16>(oh[e]) : f16_to_32<DT_FP16>(oh[e]);
-            const float y = dt == DT_BF16 ? f16_to_32<DT_BF16>(dh[e]) : f16_to_32<DT_FP16>(dh[e]);
-            acc += x * y;
-        }
-    }
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) acc += __shfl_xor(acc, m);
-    if (l16 == 0) a.dsum[lo] = acc;
 }
 
 // ---- dK, dV ---------------------------------------------------------------------------------
@@ -595,6 +556,7 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
     const uint16_t* kp = static_cast<const uint16_t*>(a.k);
     const uint16_t* vp = static_cast<const uint16_t*>(a.v);
     const uint16_t* dop = static_cast<const uint16_t*>(a.dout);
+    const uint16_t* outp = static_cast<const uint16_t*>(a.out);
 
     for (int w = blockIdx.x; w < total; w += gridDim.x) {
         const int b = bw_find_batch(s_pref, a.B, w);
@@ -628,9 +590,13 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
         const int64_t kbase = a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.k_si : (int64_t)b * a.k_sb;
         const int64_t vbase = a.cu_seqlens_k ? (int64_t)a.cu_seqlens_k[b] * a.v_si : (int64_t)b * a.v_sb;
 
-        // q and dout rows as B operands; lse (log2 units) and dsum per row
-        u32x4 qreg[RB][KSTEPS], dreg[RB][KSTEPS];
+        // q and dout rows as B operands; lse (log2 units) per row; dsum per row
+        // from the out rows and the dout rows loaded here (this kernel runs
+        // first and writes dsum for the dK/dV kernel and softmax_d)
+        const int64_t obase = a.cu_seqlens_q ? (int64_t)a.cu_seqlens_q[b] * a.o_si : (int64_t)b * a.o_sb;
+        u32x4 qreg[RB][KSTEPS], dreg[RB][KSTEPS], oreg[RB][KSTEPS];
         float lse2[RB], dsv[RB], slope[RB];
+        int64_t lor[RB];
         int qi[RB], rlo[RB], rhi[RB];  // rlo/rhi: the row's visible keys before the clamp to k_hi
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
@@ -644,7 +610,7 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
             const int64_t lo = a.cu_seqlens_q ? (int64_t)h * a.lse_sh + a.cu_seqlens_q[b] + i
                                               : (int64_t)b * a.lse_sb + (int64_t)h * a.lse_sh + i;
             lse2[rb] = ok ? a.lse[lo] * kLog2e : INFINITY;
-            dsv[rb] = ok ? a.dsum[lo] : 0.f;
+            lor[rb] = ok ? lo : -1;
             slope[rb] = (BIAS && a.alibi && ok) ? a.alibi[(int64_t)b * a.alibi_sb + h] : 0.f;
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s) {
@@ -654,9 +620,28 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
                                  : u32x4{0u, 0u, 0u, 0u};
                 dreg[rb][s] = in ? *reinterpret_cast<const u32x4*>(dop + dobase + (int64_t)i * a.do_si + (int64_t)h * a.do_sh + c * 8)
                                  : u32x4{0u, 0u, 0u, 0u};
+                oreg[rb][s] = in ? *reinterpret_cast<const u32x4*>(outp + obase + (int64_t)i * a.o_si + (int64_t)h * a.o_sh + c * 8)
+                                 : u32x4{0u, 0u, 0u, 0u};
             }
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): retire the row loads before the tile loop
+        // dsum = rowsum(dout * out): the 4 lanes li, li + 16, li + 32, li + 48 hold a row's dims
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            float acc = 0.f;
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) {
+                uint16_t oh[8], dh[8];
+                __builtin_memcpy(oh, &oreg[rb][s], 16);
+                __builtin_memcpy(dh, &dreg[rb][s], 16);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc += f16_to_32<DT>(oh[e]) * f16_to_32<DT>(dh[e]);
+            }
+            acc += __shfl_xor(acc, 16);
+            acc += __shfl_xor(acc, 32);
+            dsv[rb] = lor[rb] >= 0 ? acc : 0.f;
+            if (G == 0 && lor[rb] >= 0) a.dsum[lor[rb]] = acc;
+        }
 
         f32x4 dqa[RB][DBLK];
 #pragma unroll
@@ -827,11 +812,11 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
 // chunk tests would slow down.
 template <int DT, int HD, bool BIAS>
 static void launch_bwd_t(const BwdArgs& a, int grid_kv, int grid_q, hipStream_t stream) {
+    hipLaunchKernelGGL((fa_bwd_dq_kernel<DT, HD, BIAS>), dim3(grid_q), dim3(BwCfg<HD>::QNT), 0, stream, a);
     if (a.chunk > 0)
         hipLaunchKernelGGL((fa_bwd_dkdv_kernel<DT, HD, true, true>), dim3(grid_kv), dim3(BwCfg<HD>::KNT), 0, stream, a);
     else
         hipLaunchKernelGGL((fa_bwd_dkdv_kernel<DT, HD, BIAS, false>), dim3(grid_kv), dim3(BwCfg<HD>::KNT), 0, stream, a);
-    hipLaunchKernelGGL((fa_bwd_dq_kernel<DT, HD, BIAS>), dim3(grid_q), dim3(BwCfg<HD>::QNT), 0, stream, a);
 }
 
 template <int HD>
@@ -852,12 +837,6 @@ int bwd_row_block(int d) { return d > 128 ? BwCfg<256>::BM : d > 64 ? BwCfg<128>
 // d: kernel head dim (128 or 256); grids: upper bounds on the work items of each kernel
 hipError_t launch_bwd(const BwdArgs& a, int dtype, int d, int grid_kv, int grid_q, hipStream_t stream) {
     if (d != 64 && d != 128 && d != 256) return hipErrorInvalidValue;
-    const int64_t ntok = a.cu_seqlens_q ? (int64_t)a.total_q : (int64_t)a.B * a.Sq;
-    const int64_t rows = ntok * a.H;
-    if (rows > 0) {
-        const int64_t gsum = (rows + 15) / 16;
-        hipLaunchKernelGGL(fa_bwd_dsum_kernel, dim3((unsigned)gsum), dim3(256), 0, stream, a, dtype);
-    }
     if (d == 64) launch_bwd_d<64>(a, dtype, grid_kv, grid_q, stream);
     else if (d == 128) launch_bwd_d<128>(a, dtype, grid_kv, grid_q, stream);
     else launch_bwd_d<256>(a, dtype, grid_kv, grid_q, stream);

@@ -109,7 +109,7 @@ struct BwdArgs {
     void* dv;
     int64_t dv_sb, dv_si, dv_sh;
     const float* lse;
-    float* dsum;        // rowsum(dout * out), written by the first kernel
+    float* dsum;        // rowsum(dout * out), written by the dQ kernel (launched first)
     int64_t lse_sb, lse_sh;
     const int* cu_seqlens_q;
     const int* cu_seqlens_k;
