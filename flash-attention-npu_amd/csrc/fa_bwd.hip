@@ -201,7 +201,9 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
         const BwBatch bb = bw_batch(a, b);
         const int local = w - s_pref[b];
         const int hk = local % a.Hk;
-        const int kt = local / a.Hk;
+        // heavy first: with only a left window bound, later key blocks see more rows
+        const int nkt = (bb.sk + BK - 1) / BK;
+        const int kt = (a.wl >= 0 && a.wr < 0) ? nkt - 1 - local / a.Hk : local / a.Hk;
         const int j0 = kt * BK;
         const int g = a.g;
         const int diag0 = bb.sk - bb.sq;
@@ -563,7 +565,10 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
         const BwBatch bb = bw_batch(a, b);
         const int local = w - s_pref[b];
         const int hk = local % a.Hk;
-        const int mt = local / a.Hk;
+        // heavy first: with a right window bound (causal), later row tiles see
+        // more keys, and the hardware dispatches the workgroups in order
+        const int nmt = (bb.rows + BM - 1) / BM;
+        const int mt = a.wr >= 0 ? nmt - 1 - local / a.Hk : local / a.Hk;
         const int g = a.g;
         const int diag0 = bb.sk - bb.sq;
         const int tile_row0 = mt * BM;
