@@ -29,6 +29,7 @@
 // dS and P are rounded to the input type before their MFMAs.
 #include "fa_common.h"
 #include "fa_kernel_args.h"
+#include "fa_udiv.h"
 
 #include <type_traits>
 
@@ -206,6 +207,7 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
         const int kt = (a.wl >= 0 && a.wr < 0) ? nkt - 1 - local / a.Hk : local / a.Hk;
         const int j0 = kt * BK;
         const int g = a.g;
+        const UDiv gd = udiv_make((uint32_t)g);  // r / g by a multiply-high in the tile loop
         const int diag0 = bb.sk - bb.sq;
         const int64_t qbase = a.cu_seqlens_q ? (int64_t)a.cu_seqlens_q[b] * a.q_si : (int64_t)b * a.q_sb;
         const int64_t dobase = a.cu_seqlens_q ? (int64_t)a.cu_seqlens_q[b] * a.do_si : (int64_t)b * a.do_sb;
@@ -280,7 +282,7 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
             for (int u = 0; u < CPQ; ++u) {
                 const int r = r0 + rr0 + u * (NT / DCH);
                 if (r < r_hi && dch * 8 < a.hd) {
-                    const int i = r / g, h = hk * g + r % g;
+                    const int i = (int)udiv(gd, (uint32_t)r), h = hk * g + (r - i * g);
                     qr[u] = *reinterpret_cast<const u32x4*>(qp + qbase + (int64_t)i * a.q_si + (int64_t)h * a.q_sh + dch * 8);
                     dr[u] = *reinterpret_cast<const u32x4*>(dop + dobase + (int64_t)i * a.do_si + (int64_t)h * a.do_sh + dch * 8);
                 } else {
@@ -291,7 +293,7 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
             if (tid < BQ) {
                 const int r = r0 + tid;
                 if (r < r_hi) {
-                    const int i = r / g, h = hk * g + r % g;
+                    const int i = (int)udiv(gd, (uint32_t)r), h = hk * g + (r - i * g);
                     const int64_t lo = a.cu_seqlens_q ? (int64_t)h * a.lse_sh + a.cu_seqlens_q[b] + i
                                                       : (int64_t)b * a.lse_sb + (int64_t)h * a.lse_sh + i;
                     lr = a.lse[lo] * kLog2e;
@@ -461,7 +463,7 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
                 for (int hh = 0; hh < 2; ++hh) {
                     const int h0 = rt + 32 * hh;  // first packed row of the half
                     if (h0 >= r_hi) continue;
-                    const int p_lo = h0 / g, p_hi = min(h0 + 31, r_hi - 1) / g;
+                    const int p_lo = (int)udiv(gd, (uint32_t)h0), p_hi = (int)udiv(gd, (uint32_t)min(h0 + 31, r_hi - 1));
                     if (p_hi < wi_lo || p_lo > wi_hi) continue;  // no row of the half sees these keys
                     bool full = h0 + 32 <= r_hi && jw + WK <= bb.sk;
                     if (a.wr >= 0 && jw + WK - 1 > p_lo + diag0 + a.wr) full = false;

@@ -43,3 +43,19 @@ def test_decode_split_against_brute_force(tmp_path):
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, (r.stdout + r.stderr)[-4000:]
     assert " 0 failures" in r.stdout, r.stdout
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+def test_invariant_division_against_plain_division(tmp_path):
+    """The multiply-high division by a run-time invariant divisor that the
+    backward's tile loop uses for packed row -> query position
+    (csrc/fa_udiv.h, host and device code alike) against n / d, under
+    ASan / UBSan."""
+    exe = tmp_path / "udiv_check"
+    cmd = ["g++", "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+           "-I", CSRC, os.path.join(REPO, "tests", "host", "fa_udiv_check.cpp"), "-o", str(exe)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-4000:]
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, (r.stdout + r.stderr)[-4000:]
+    assert " 0 failures" in r.stdout, r.stdout
