@@ -312,6 +312,21 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
             kb0 += row0k;
             vb0 += row0v;
         }
+        // contiguous / varlen: this thread's key rows of the next tile as
+        // element offsets from kb0 / vb0, moved BN keys on per load_tile call
+        // (the calls load the tiles at k_lo, k_lo + BN, ... in that order), so
+        // the tile loop does no 64-bit products
+        [[maybe_unused]] int64_t kcur[CPT], vcur[CPT], kstep = 0, vstep = 0;
+        if constexpr (!PAGED) {
+#pragma unroll
+            for (int u = 0; u < CPT; ++u) {
+                const int j = k_lo + kk0 + u * (NT / DCH);
+                kcur[u] = (int64_t)j * a.k_si;
+                vcur[u] = (int64_t)j * a.v_si;
+            }
+            kstep = (int64_t)BN * a.k_si;
+            vstep = (int64_t)BN * a.v_si;
+        }
         auto load_tile = [&](int t0) {
 #pragma unroll
             for (int u = 0; u < CPT; ++u) {
@@ -326,14 +341,18 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
                         kpr = kb0 + (int64_t)blk * a.k_sb + (int64_t)inp * a.k_si;
                         vpr = vb0 + (int64_t)blk * a.v_sb + (int64_t)inp * a.v_si;
                     } else {
-                        kpr = kb0 + (int64_t)j * a.k_si;
-                        vpr = vb0 + (int64_t)j * a.v_si;
+                        kpr = kb0 + kcur[u];
+                        vpr = vb0 + vcur[u];
                     }
                     kr[u] = *reinterpret_cast<const RT*>(kpr);
                     vr[u] = *reinterpret_cast<const RT*>(vpr);
                 } else {
                     kr[u] = RT{};
                     vr[u] = RT{};
+                }
+                if constexpr (!PAGED) {
+                    kcur[u] += kstep;
+                    vcur[u] += vstep;
                 }
             }
         };
