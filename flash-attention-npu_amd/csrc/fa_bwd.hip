@@ -132,7 +132,7 @@ __device__ __forceinline__ float bw_score(const BwdArgs& a, float x, float slope
         float y = x * a.scale;
         t = 0.f;
         if (a.softcap > 0.f) {
-            t = tanhf(y / a.softcap);
+            t = fast_tanh(y * (1.f / a.softcap));
             y = a.softcap * t;
         }
         if (a.alibi) y -= slope * (float)(dist < 0 ? -dist : dist);

@@ -142,6 +142,14 @@ __device__ __forceinline__ int split_addr128(int r, int c, int h) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+// tanh(z) = 1 - 2 / (e^(2z) + 1) on the hardware exp2 and reciprocal: absolute
+// error ~1e-7 over the whole range, +-1 exactly once e^(2z) over- or underflows
+// (|z| > ~44); used for the soft cap, where cap * tanh enters exp() as an
+// absolute score, so an absolute error of cap * 1e-7 is what matters.
+__device__ __forceinline__ float fast_tanh(float z) {
+    const float e = fast_exp2(z * (2.f * kLog2e));
+    return 1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f);
+}
 
 __device__ __forceinline__ float wave_max16x4(float v) {
     // max over the 4 lanes l, l^16, l^32, l^48 that hold the same MFMA column

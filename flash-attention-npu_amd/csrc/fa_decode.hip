@@ -557,7 +557,7 @@ __global__ void __launch_bounds__(256, 1) fa_decode_kernel(FwdArgs a) {
                     xv = sv2 * (F8 ? sc_qk2 : a.scale_log2);
                 } else {
                     float y = sv2 * (F8 ? sc_qk : a.scale);
-                    if (a.softcap > 0.f) y = a.softcap * tanhf(y / a.softcap);
+                    if (a.softcap > 0.f) y = a.softcap * fast_tanh(y * (1.f / a.softcap));
                     if (a.alibi) {
                         int dist = qi + diag0 - (key0 + h * 16 + G * 4 + e);
                         dist = dist < 0 ? -dist : dist;

@@ -505,7 +505,7 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
                         const int j = s0 + kb * 16 + G * 4 + e;
                         if constexpr (BIAS) {
                             float y = x * sc_qk;
-                            if (a.softcap > 0.f) y = a.softcap * tanhf(y / a.softcap);
+                            if (a.softcap > 0.f) y = a.softcap * fast_tanh(y * (1.f / a.softcap));
                             if (a.alibi) {
                                 int dist = qi[rb] + diag0 - j;
                                 dist = dist < 0 ? -dist : dist;
