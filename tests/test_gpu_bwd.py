@@ -286,3 +286,15 @@ def test_bwd_v3_unaligned_headdim(D):
     # the v3 API runs head dims that are not a multiple of 8 zero-padded; the
     # gradients flow back through the padding
     run_dense(torch.bfloat16, 2, 4, 2, 200, 260, D, True, api="v3", seed=30 + D)
+
+
+# GQA ratios that do not divide the dK/dV kernel's 64-row tiles: its per-thread
+# row cursors move 64 packed rows per tile as 64 // g positions and 64 % g heads
+# and carry a position when the head offset wraps; enough row tiles per key
+# block that the wraps accumulate, and a left-only window for the reversed
+# key-block order
+@pytest.mark.parametrize("g", [3, 5, 7])
+def test_bwd_gqa_ratio_not_dividing_row_tile(g):
+    run_dense(torch.bfloat16, 1, 2 * g, 2, 700, 700, 128, True, seed=60 + g)
+    run_dense(torch.float16, 2, g, 1, 333, 517, 64, False, window=(100, -1), seed=70 + g)
+    run_varlen(torch.bfloat16, 2 * g, 2, [700, 1, 129], [700, 64, 300], 128, True, seed=80 + g)
