@@ -282,7 +282,13 @@ void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
         if (!pl.allow_split) pl.items_max = base_bound;
         else if (p->num_splits > 1) pl.items_max = base_bound * p->num_splits;
         else pl.items_max = base_bound + pl.target_items;
+        // Without a split, sequences of one length (no cu_seqlens_q) run on
+        // occ * cus workgroups that each take several items, paired heavy with
+        // light by the kernel's alternating passes: no workgroup start-up per
+        // item. Ragged query lengths keep one workgroup per item, which the
+        // hardware hands out heaviest first as CUs free up.
         if (pl.allow_split) pl.grid = (int)std::min<int64_t>(pl.items_max, (int64_t)occ * cus);
+        else if (!p->cu_seqlens_q) pl.grid = (int)std::min<int64_t>(pl.items_max, (int64_t)occ * cus);
         else pl.grid = (int)std::min<int64_t>(pl.items_max, INT_MAX);
         if (pl.grid < 1) pl.grid = 1;
     }

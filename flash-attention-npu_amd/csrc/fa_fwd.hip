@@ -239,7 +239,12 @@ __global__ void __launch_bounds__(PfCfg<HD>::NT, 1) fa_prefill_kernel(FwdArgs a)
     uint16_t* op = static_cast<uint16_t*>(a.out);
     const float cs = a.scale_log2;
 
-    for (int w = blockIdx.x; w < total; w += gridDim.x) {
+    // Pass k takes item k * grid + blockIdx.x, in the other direction on odd
+    // passes, so a workgroup's heavy item of one pass pairs with a light one of
+    // the next (items are numbered heaviest first within a sequence).
+    for (int k = 0; k * (int)gridDim.x < total; ++k) {
+        const int w = k * (int)gridDim.x + ((k & 1) ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x);
+        if (w >= total) continue;
         // ---- decode the work item ------------------------------------------------------
         int bl = 0, bh = a.B;
         while (bh - bl > 1) {
