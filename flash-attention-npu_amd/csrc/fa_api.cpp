@@ -701,7 +701,10 @@ fa_status_t run_backward(const fa_bwd_params* p, int kind, void* stream_v) {
         const int64_t gkv = (int64_t)nb * p->nheads_k * (((int64_t)p->seqlen_k + fa::bwd_key_block(kd) - 1) / fa::bwd_key_block(kd));
         const int64_t gq = (int64_t)nb * p->nheads_k *
                            (((int64_t)p->seqlen_q * a.g + fa::bwd_row_block(kd) - 1) / fa::bwd_row_block(kd));
-        const int cap = 16 * cu_count();  // the kernels walk their work items in a grid-stride loop
+        // the kernels walk their work items in alternating passes over the
+        // grid: same-length sequences run on 2 x CUs workgroups of several
+        // items each, ragged ones on one workgroup per item (up to 16 x CUs)
+        const int cap = (p->cu_seqlens_q ? 16 : 2) * cu_count();
         const int grid_kv = (int)std::max<int64_t>(1, std::min<int64_t>(gkv, cap));
         const int grid_q = (int)std::max<int64_t>(1, std::min<int64_t>(gq, cap));
         hipError_t e = fa::launch_bwd(a, p->dtype, kd, grid_kv, grid_q, static_cast<hipStream_t>(stream_v));

@@ -197,7 +197,11 @@ __global__ void __launch_bounds__(BwCfg<HD>::KNT, 1) fa_bwd_dkdv_kernel(BwdArgs 
     const uint16_t* vp = static_cast<const uint16_t*>(a.v);
     const uint16_t* dop = static_cast<const uint16_t*>(a.dout);
 
-    for (int w = blockIdx.x; w < total; w += gridDim.x) {
+    // pass k takes item k * grid + blockIdx.x, the other way round on odd
+    // passes (a heavy item of one pass pairs with a light one of the next)
+    for (int k = 0; k * (int)gridDim.x < total; ++k) {
+        const int w = k * (int)gridDim.x + ((k & 1) ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x);
+        if (w >= total) continue;
         const int b = bw_find_batch(s_pref, a.B, w);
         const BwBatch bb = bw_batch(a, b);
         const int local = w - s_pref[b];
@@ -640,7 +644,11 @@ __global__ void __launch_bounds__(BwCfg<HD>::QNT, 1) fa_bwd_dq_kernel(BwdArgs a)
     const uint16_t* dop = static_cast<const uint16_t*>(a.dout);
     const uint16_t* outp = static_cast<const uint16_t*>(a.out);
 
-    for (int w = blockIdx.x; w < total; w += gridDim.x) {
+    // pass k takes item k * grid + blockIdx.x, the other way round on odd
+    // passes (a heavy item of one pass pairs with a light one of the next)
+    for (int k = 0; k * (int)gridDim.x < total; ++k) {
+        const int w = k * (int)gridDim.x + ((k & 1) ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x);
+        if (w >= total) continue;
         const int b = bw_find_batch(s_pref, a.B, w);
         const BwBatch bb = bw_batch(a, b);
         const int local = w - s_pref[b];
