@@ -283,12 +283,13 @@ void make_plan(const fa_fwd_params* p, int kind, Plan& pl) {
         else if (p->num_splits > 1) pl.items_max = base_bound * p->num_splits;
         else pl.items_max = base_bound + pl.target_items;
         // Without a split, sequences of one length (no cu_seqlens_q) run on
-        // occ * cus workgroups that each take several items, paired heavy with
+        // one workgroup per CU that takes several items, paired heavy with
         // light by the kernel's alternating passes: no workgroup start-up per
-        // item. Ragged query lengths keep one workgroup per item, which the
-        // hardware hands out heaviest first as CUs free up.
+        // item (1-4.5 % faster than 2 workgroups per CU on dense shapes).
+        // Ragged query lengths keep one workgroup per item, which the hardware
+        // hands out heaviest first as CUs free up.
         if (pl.allow_split) pl.grid = (int)std::min<int64_t>(pl.items_max, (int64_t)occ * cus);
-        else if (!p->cu_seqlens_q) pl.grid = (int)std::min<int64_t>(pl.items_max, (int64_t)occ * cus);
+        else if (!p->cu_seqlens_q) pl.grid = (int)std::min<int64_t>(pl.items_max, (int64_t)cus);
         else pl.grid = (int)std::min<int64_t>(pl.items_max, INT_MAX);
         if (pl.grid < 1) pl.grid = 1;
     }
@@ -702,9 +703,11 @@ fa_status_t run_backward(const fa_bwd_params* p, int kind, void* stream_v) {
         const int64_t gq = (int64_t)nb * p->nheads_k *
                            (((int64_t)p->seqlen_q * a.g + fa::bwd_row_block(kd) - 1) / fa::bwd_row_block(kd));
         // the kernels walk their work items in alternating passes over the
-        // grid: same-length sequences run on 2 x CUs workgroups of several
-        // items each, ragged ones on one workgroup per item (up to 16 x CUs)
-        const int cap = (p->cu_seqlens_q ? 16 : 2) * cu_count();
+        // grid: same-length sequences run on one workgroup per CU taking
+        // several items each (B4 S4096 H32/8 causal the same as with 2 x CUs
+        // workgroups, B2 3-4 % faster), ragged ones on one workgroup per item
+        // (up to 16 x CUs)
+        const int cap = (p->cu_seqlens_q ? 16 : 1) * cu_count();
         const int grid_kv = (int)std::max<int64_t>(1, std::min<int64_t>(gkv, cap));
         const int grid_q = (int)std::max<int64_t>(1, std::min<int64_t>(gq, cap));
         hipError_t e = fa::launch_bwd(a, p->dtype, kd, grid_kv, grid_q, static_cast<hipStream_t>(stream_v));
